@@ -1,0 +1,228 @@
+"""Benchmark of the cmpext3 GEMM path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME] [--no-cpu] [--no-others]
+
+One "step" is one call of the operator (cmpext3.fp16_matmul etc.) on inputs
+already resident in HBM.  The headline workload is BASELINE.json's metric
+configuration, fp16 4096^3 (cfg2); the line also carries the other GPU
+configurations (bf16 MLP up-projection, fp16 M=16 skinny, ragged fp32) timed
+the same way.  Rank 0 prints ONE JSON line.
+
+roofline: algorithmic FLOP (2*M*N*K) or bytes (A + B + C once) per launch of
+the dominant kernel, divided by its average duration measured with HIP events
+on the stream the kernel runs on (PyTorch's current stream), against MI355X's
+published peaks (dense fp16/bf16 MFMA 2516.6 TFLOP/s, fp32 MFMA 157.3 TFLOP/s,
+HBM3E 8 TB/s).  `traffic` (HBM bytes per launch) comes from the committed
+rocprofv3 FETCH_SIZE/WRITE_SIZE summary in profiles/hbm_traffic.json when it
+has an entry for the workload, else null.
+
+cpu_baseline: the reference CPU path that BASELINE.json names -- the same op
+via torch.matmul on CPU tensors (oracle.gemm_oracle.cpu_matmul), timed on this
+host's cores over a bounded sample (about 10 s).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "GEMM TFLOPS + % of MI355X dense peak (fp16/bf16 4096³); GB/s at M=16"
+PEAK = {"fp16": 2516.6, "bf16": 2516.6, "fp32": 157.3}   # TFLOP/s, dense
+HBM_PEAK_GBS = 8000.0
+
+CONFIGS = {
+    "cfg2_fp16_4096": dict(dtype="fp16", M=4096, N=4096, K=4096, dist="normal", scale=1.0 / 64.0,
+                           desc="fp16_matmul 4096x4096x4096"),
+    "cfg3_bf16_mlp": dict(dtype="bf16", M=4096, N=14336, K=4096, dist="normal", scale=0.02,
+                          desc="bf16_matmul 4096x4096 @ 4096x14336 (MLP up-projection)"),
+    "cfg4_fp16_skinny": dict(dtype="fp16", M=16, N=8192, K=8192, dist="normal", scale=8192 ** -0.5,
+                             desc="fp16_matmul 16x8192 @ 8192x8192 (decode, HBM-bound)", hbm=True),
+    "cfg5_fp32_ragged": dict(dtype="fp32", M=4097, N=3001, K=2049, dist="uniform",
+                             desc="fp32_matmul 4097x2049 @ 2049x3001 (ragged)"),
+}
+HEADLINE = "cfg2_fp16_4096"
+
+
+def algorithmic(c) -> tuple[float, float]:
+    esz = 4 if c["dtype"] == "fp32" else 2
+    flops = 2.0 * c["M"] * c["N"] * c["K"]
+    nbytes = float(esz * (c["M"] * c["K"] + c["K"] * c["N"] + c["M"] * c["N"]))
+    return flops, nbytes
+
+
+def make_gpu_inputs(c, nb: int, seed: int = 0):
+    import torch
+
+    dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[c["dtype"]]
+    g = torch.Generator(device="cuda").manual_seed(seed)
+
+    def draw(shape):
+        if c["dist"] == "uniform":
+            return (torch.rand(shape, generator=g, device="cuda") * 2 - 1).to(dt)
+        return (torch.randn(shape, generator=g, device="cuda") * c["scale"]).to(dt)
+
+    a = draw((c["M"], c["K"]))
+    bs = [draw((c["K"], c["N"])) for _ in range(nb)]
+    return a, bs
+
+
+def time_gpu(name: str, steps: int, warmup: int) -> dict:
+    import torch
+
+    import cmpext3
+
+    c = CONFIGS[name]
+    fn = {"fp16": cmpext3.fp16_matmul, "bf16": cmpext3.bf16_matmul, "fp32": cmpext3.fp32_matmul}[c["dtype"]]
+    # The skinny config streams all of B; its 128 MiB would stay in the 256 MB
+    # Infinity Cache across calls, so it cycles through 4 distinct B buffers.
+    nb = 4 if c.get("hbm") else 1
+    a, bs = make_gpu_inputs(c, nb)
+    for i in range(warmup):
+        fn(a, bs[i % nb])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(steps):
+        fn(a, bs[i % nb])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    wall_ms = (t1 - t0) * 1e3 / steps
+    kern_ms = e0.elapsed_time(e1) / steps
+    flops, nbytes = algorithmic(c)
+    r = dict(config=name, desc=c["desc"], dtype=c["dtype"], kernel=cmpext3.plan(c["dtype"], c["M"], c["N"], c["K"]).split()[0].split("=")[1],
+             ms_per_step=wall_ms, kernel_ms=kern_ms,
+             tflops=flops / (wall_ms * 1e-3) / 1e12, kernel_tflops=flops / (kern_ms * 1e-3) / 1e12,
+             gbs=nbytes / (wall_ms * 1e-3) / 1e9, kernel_gbs=nbytes / (kern_ms * 1e-3) / 1e9)
+    del a, bs
+    torch.cuda.empty_cache()
+    return r
+
+
+def cpu_baseline(name: str, budget_s: float = 10.0) -> dict:
+    """The reference CPU path (torch.matmul on CPU) on the same workload."""
+    import platform
+
+    import torch
+
+    from oracle.gemm_oracle import cpu_matmul, make_inputs
+
+    c = CONFIGS[name]
+    a, b = make_inputs(c["dtype"], c["M"], c["N"], c["K"], c["dist"], c.get("scale", 1.0), 0)
+    cpu_matmul(a, b)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while (len(times) < 3 or time.perf_counter() - t_start < budget_s) and len(times) < 50:
+        t0 = time.perf_counter()
+        cpu_matmul(a, b)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    flops, nbytes = algorithmic(c)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        model = platform.processor()
+    hbm = c.get("hbm")
+    return {"value": (nbytes / med / 1e9) if hbm else (flops / med / 1e12),
+            "unit": "GB/s" if hbm else "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{c['desc']} via torch.matmul on CPU ({c['dtype']}), full size, median of {len(times)} "
+                      f"calls after 1 warm-up ({med * 1e3:.1f} ms/call); os.cpu_count()={os.cpu_count()}; {model}"}
+
+
+def load_traffic(name: str):
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        entry = data.get(name)
+        return None if entry is None else float(entry["bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def roofline(r: dict, name: str) -> dict:
+    c = CONFIGS[name]
+    if c.get("hbm"):
+        ach, peak, unit, bound = r["kernel_gbs"], HBM_PEAK_GBS, "GB/s", "hbm"
+    else:
+        ach, peak, unit, bound = r["kernel_tflops"], PEAK[c["dtype"]], "TFLOP/s", "mfma"
+    return {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
+            "frac": round(ach / peak, 4), "traffic": load_traffic(name), "kernel": r["kernel"],
+            "kernel_ms": round(r["kernel_ms"], 5)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default=HEADLINE, choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-others", action="store_true", help="time only the headline workload")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the GEMM path has no multi-GPU "
+              "component); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import cmpext3  # noqa: F401  (fails loudly if the extension is missing)
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    head = time_gpu(args.config, args.steps, args.warmup)
+    others = {}
+    if not args.no_others:
+        for name in CONFIGS:
+            if name != args.config:
+                r = time_gpu(name, args.steps, args.warmup)
+                c = CONFIGS[name]
+                others[name] = {"desc": r["desc"], "kernel": r["kernel"], "ms_per_step": round(r["ms_per_step"], 5),
+                                **({"GB/s": round(r["gbs"], 1)} if c.get("hbm") else
+                                   {"TFLOP/s": round(r["tflops"], 2)}),
+                                "roofline": roofline(r, name)}
+    c = CONFIGS[args.config]
+    hbm = c.get("hbm")
+    line = {
+        "metric": METRIC,
+        "value": round(head["gbs"] if hbm else head["tflops"], 3),
+        "unit": "GB/s" if hbm else "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"fp16": "f16", "bf16": "bf16", "fp32": "f32"}[c["dtype"]],
+        "data": "synthetic (seeded torch.randn / torch.rand on the GPU, BASELINE.json distributions)",
+        "config": {"workload": f"{args.config}: {c['desc']}", "M": c["M"], "N": c["N"], "K": c["K"],
+                   "accumulate": "fp32", "kernel": head["kernel"]},
+        "roofline": roofline(head, args.config),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.config)
+    if others:
+        line["other_configs"] = others
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,34 @@
+"""cmpext3 dense GEMM operators for AMD Instinct MI355X (gfx950).
+
+Python surface (same names and argument meaning as the reference extension's
+GEMM entry points, src/main.cpp:1594-1602, plus the dtype-specific matmuls):
+
+    fp16_matmul(a, b), bf16_matmul(a, b), fp32_matmul(a, b)   C = A @ B
+    linear(input, weight, bias=None)                          input @ weight.T + bias
+    bmm(input, mat2)                                           batched A @ B
+    plan(dtype, M, N, K, layout="KN", batch=1, has_bias=False) kernel the selector picks
+
+Every call runs the hand-written gfx950 kernels of lib/libcmpext3_gemm.so on
+PyTorch's current stream.  There is no fallback: if the compiled extension is
+missing, importing this package raises ImportError.
+"""
+import torch  # noqa: F401  (loads PyTorch's HIP runtime before the extension binds to it)
+
+try:
+    from . import _cmpext3 as _ext
+except ImportError as e:  # pragma: no cover - exercised only on a tree that was not built
+    raise ImportError(
+        "cmp_ext_amd: the compiled extension is missing; run `python -m cmp_ext_amd.build` "
+        f"(or __graft_entry__.build()) first ({e})"
+    ) from e
+
+fp16_matmul = _ext.fp16_matmul
+bf16_matmul = _ext.bf16_matmul
+fp32_matmul = _ext.fp32_matmul
+linear = _ext.linear
+bmm = _ext.bmm
+plan = _ext.plan
+version = _ext.version
+extension_path = _ext.__file__
+
+__all__ = ["fp16_matmul", "bf16_matmul", "fp32_matmul", "linear", "bmm", "plan", "version"]

@@ -1,0 +1,88 @@
+"""ctypes view of the C ABI in include/cmpext3_gemm.h (libcmpext3_gemm.so).
+
+Used by the tests and the benchmark to drive the kernels through the same
+boundary a non-Python caller would bind.  PyTorch is imported first so that
+the library binds to PyTorch's HIP runtime (a second runtime in the process
+would not understand PyTorch's stream handles).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libcmpext3_gemm.so")
+
+F16, BF16, F32 = 0, 1, 2
+B_KN, B_NK = 0, 1
+OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_TOO_LARGE = 0, -1, -2, -3
+
+# Exported symbols and their C signatures, as declared in include/cmpext3_gemm.h.
+_i, _i64, _p, _cp = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_char_p
+SIGNATURES = {
+    "cmpext3_matmul_fp16": (_i, [_p, _p, _p, _i, _i, _i, _p]),
+    "cmpext3_matmul_bf16": (_i, [_p, _p, _p, _i, _i, _i, _p]),
+    "cmpext3_matmul_fp32": (_i, [_p, _p, _p, _i, _i, _i, _p]),
+    "cmpext3_gemm_ex": (_i, [_i, _i, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p,
+                             _i, _i, _i, _i, _p]),
+    "cmpext3_gemm_plan": (_i, [_i, _i, _i, _i, _i, _i64, _i64, _i64, _i, _i, _i, _cp, _i]),
+    "cmpext3_status_string": (_cp, [_i]),
+    "cmpext3_version": (_cp, []),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise OSError(f"{LIB_PATH} not built; run `python -m cmp_ext_amd.build`")
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(l, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = l
+    return _lib
+
+
+def status_string(st: int) -> str:
+    return lib().cmpext3_status_string(st).decode()
+
+
+def plan(dtype: int, layout: int, M: int, N: int, K: int, lda: int | None = None,
+         ldb: int | None = None, ldc: int | None = None, align: int = 16, has_bias: bool = False,
+         batch: int = 1) -> tuple[int, str]:
+    lda = max(K, 1) if lda is None else lda
+    ldb = max(N if layout == B_KN else K, 1) if ldb is None else ldb
+    ldc = max(N, 1) if ldc is None else ldc
+    buf = ctypes.create_string_buffer(256)
+    kid = lib().cmpext3_gemm_plan(dtype, layout, M, N, K, lda, ldb, ldc, align, int(has_bias), batch,
+                                  buf, 256)
+    return kid, buf.value.decode()
+
+
+def _stream_handle(stream) -> int:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+def gemm_ex(dtype: int, layout: int, A, lda: int, stride_a: int, B, ldb: int, stride_b: int, C,
+            ldc: int, stride_c: int, bias, M: int, N: int, K: int, batch: int = 1, stream=None) -> int:
+    """Call cmpext3_gemm_ex with raw device pointers (ints) or tensors."""
+    def ptr(x):
+        if x is None:
+            return None
+        return x.data_ptr() if hasattr(x, "data_ptr") else int(x)
+    return lib().cmpext3_gemm_ex(dtype, layout, ptr(A), lda, stride_a, ptr(B), ldb, stride_b, ptr(C),
+                                 ldc, stride_c, ptr(bias), M, N, K, batch, _stream_handle(stream))
+
+
+def matmul(dtype: int, A, B, C, M: int, N: int, K: int, stream=None) -> int:
+    """Call cmpext3_matmul_{fp16,bf16,fp32} (packed row-major operands)."""
+    fn = {F16: lib().cmpext3_matmul_fp16, BF16: lib().cmpext3_matmul_bf16,
+          F32: lib().cmpext3_matmul_fp32}[dtype]
+    return fn(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, _stream_handle(stream))

@@ -1,0 +1,159 @@
+// C ABI of the gfx950 GEMM library (declared in include/cmpext3_gemm.h).
+// Validates, asks the selector for a plan and launches one kernel per call
+// (or one per 65535 batch entries) on the caller's stream.
+#include <hip/hip_runtime_api.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "../../include/cmpext3_gemm.h"
+#include "kernels.h"
+#include "selector.h"
+
+using namespace cmpext3;
+
+namespace {
+
+int align_of(const void* ptr) {
+  const uintptr_t v = (uintptr_t)ptr;
+  if (v == 0) return 16;
+  int a = 1;
+  while (a < 16 && v % (uintptr_t)(2 * a) == 0) a *= 2;
+  return a;
+}
+
+hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p, dim3 grid,
+                    hipStream_t s) {
+  const BLayout lay = (BLayout)layout;
+  switch (plan.kernel) {
+    case kTile256x256:
+    case kTile256x224:
+    case kTile128x128:
+      return dtype == kF16 ? launch_tile_f16(plan.kernel, lay, p, grid, s)
+                           : launch_tile_bf16(plan.kernel, lay, p, grid, s);
+    case kSkinny:
+      return launch_skinny((DType)dtype, plan.mb, p, grid, s);
+    case kF32Tile128:
+    case kF32Tile64:
+      return launch_f32(plan.kernel, lay, p, grid, s);
+    case kGeneric16:
+      return launch_generic((DType)dtype, lay, p, grid, s);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+constexpr int64_t kMaxGridZ = 65535;
+
+}  // namespace
+
+extern "C" int cmpext3_gemm_ex(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride_a,
+                               const void* B, int64_t ldb, int64_t stride_b, void* C, int64_t ldc,
+                               int64_t stride_c, const void* bias, int M, int N, int K, int batch,
+                               void* stream) {
+  Request r{};
+  r.dtype = dtype;
+  r.layout = b_layout;
+  r.M = M;
+  r.N = N;
+  r.K = K;
+  r.lda = lda;
+  r.ldb = ldb;
+  r.ldc = ldc;
+  r.stride_a = stride_a;
+  r.stride_b = stride_b;
+  r.stride_c = stride_c;
+  r.align = std::min(std::min(align_of(A), align_of(B)), std::min(align_of(C), align_of(bias)));
+  r.has_bias = bias != nullptr;
+  r.batch = batch;
+  Plan plan;
+  const int st = make_plan(r, &plan);
+  if (st != CMPEXT3_OK) return st;
+  if (M == 0 || N == 0 || batch == 0) return CMPEXT3_OK;
+  if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return CMPEXT3_ERR_INVALID_ARG;
+
+  const int64_t esz = dtype == kF32 ? 4 : 2;
+  GemmParams p{};
+  p.bias = bias;
+  p.lda = lda;
+  p.ldb = ldb;
+  p.ldc = ldc;
+  p.stride_a = stride_a;
+  p.stride_b = stride_b;
+  p.stride_c = stride_c;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.tiles_m = plan.tiles_m;
+  p.tiles_n = plan.tiles_n;
+  p.group_m = plan.group_m;
+  p.k_per_wave = plan.k_per_wave;
+  hipStream_t s = (hipStream_t)stream;
+  for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridZ) {
+    const int64_t nb = std::min<int64_t>(kMaxGridZ, batch - b0);
+    p.A = (const char*)A + b0 * stride_a * esz;
+    p.B = (const char*)B + b0 * stride_b * esz;
+    p.C = (char*)C + b0 * stride_c * esz;
+    const dim3 grid((unsigned)(plan.tiles_m * plan.tiles_n), 1, (unsigned)nb);
+    const hipError_t e = dispatch(plan, dtype, b_layout, p, grid, s);
+    if (e != hipSuccess) return (int)e;
+  }
+  return CMPEXT3_OK;
+}
+
+extern "C" int cmpext3_matmul_fp16(const void* A, const void* B, void* C, int M, int N, int K, void* stream) {
+  return cmpext3_gemm_ex(CMPEXT3_F16, CMPEXT3_B_KN, A, K > 1 ? K : 1, 0, B, N > 1 ? N : 1, 0, C, N > 1 ? N : 1, 0,
+                         nullptr, M, N, K, 1, stream);
+}
+
+extern "C" int cmpext3_matmul_bf16(const void* A, const void* B, void* C, int M, int N, int K, void* stream) {
+  return cmpext3_gemm_ex(CMPEXT3_BF16, CMPEXT3_B_KN, A, K > 1 ? K : 1, 0, B, N > 1 ? N : 1, 0, C, N > 1 ? N : 1, 0,
+                         nullptr, M, N, K, 1, stream);
+}
+
+extern "C" int cmpext3_matmul_fp32(const float* A, const float* B, float* C, int M, int N, int K, void* stream) {
+  return cmpext3_gemm_ex(CMPEXT3_F32, CMPEXT3_B_KN, A, K > 1 ? K : 1, 0, B, N > 1 ? N : 1, 0, C, N > 1 ? N : 1, 0,
+                         nullptr, M, N, K, 1, stream);
+}
+
+extern "C" int cmpext3_gemm_plan(int dtype, int b_layout, int M, int N, int K, int64_t lda, int64_t ldb,
+                                 int64_t ldc, int align, int has_bias, int batch, char* buf, int buflen) {
+  Request r{};
+  r.dtype = dtype;
+  r.layout = b_layout;
+  r.M = M;
+  r.N = N;
+  r.K = K;
+  r.lda = lda;
+  r.ldb = ldb;
+  r.ldc = ldc;
+  r.stride_a = (int64_t)M * lda;
+  r.stride_b = (int64_t)(b_layout == CMPEXT3_B_KN ? K : N) * ldb;
+  r.stride_c = (int64_t)M * ldc;
+  r.align = align;
+  r.has_bias = has_bias != 0;
+  r.batch = batch;
+  Plan plan;
+  const int st = make_plan(r, &plan);
+  if (st != CMPEXT3_OK) return st;
+  if (buf && buflen > 0) {
+    const std::string d = describe(r, plan);
+    strncpy(buf, d.c_str(), (size_t)buflen - 1);
+    buf[buflen - 1] = '\0';
+  }
+  return (int)plan.kernel;
+}
+
+extern "C" const char* cmpext3_status_string(int status) {
+  switch (status) {
+    case CMPEXT3_OK: return "success";
+    case CMPEXT3_ERR_INVALID_ARG: return "invalid argument (null pointer, negative size or leading dimension too small)";
+    case CMPEXT3_ERR_UNSUPPORTED: return "unsupported dtype or B layout";
+    case CMPEXT3_ERR_TOO_LARGE: return "size or leading dimension exceeds the kernels' 32-bit offset range";
+    default:
+      if (status > 0) return hipGetErrorString((hipError_t)status);
+      return "unknown status";
+  }
+}
+
+extern "C" const char* cmpext3_version(void) { return "cmpext3-mi355x 0.1.0 (gfx950)"; }

@@ -1,0 +1,172 @@
+// Device helpers shared by the gfx950 GEMM kernels: operand vector types,
+// MFMA wrappers, buffer-resource loads with hardware zero-fill, the LDS
+// swizzle, the 8x8 16-bit register transpose and the XCD-aware tile order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gemm_params.h"
+
+namespace cmpext3 {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Offset that is always outside a buffer resource whose num_records is
+// kBufRecords: a buffer load with it returns zeros and touches no memory.
+constexpr uint32_t kBufRecords = 0x7FFFFFFFu;
+constexpr uint32_t kBufOOB = 0x80000000u;
+
+// gfx9 buffer descriptor word 3 (32-bit untyped access).
+constexpr int kBufWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)kBufRecords, kBufWord3);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+}
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers.  The products are issued "swapped": the first MFMA operand
+// carries B (its rows are output columns n), the second carries A (its
+// columns are output rows m).  The 16x16 result block D[n][m] = C[m][n] then
+// lands with lane l holding C[m = l%16][n = 4*(l/16) + i], i = 0..3: four
+// consecutive columns of one row, which is the layout the epilogue stores.
+// ---------------------------------------------------------------------------
+template <typename T> struct Mfma;
+
+template <> struct Mfma<_Float16> {
+  static __device__ __forceinline__ f32x4 mma(u32x4 b, u32x4 a, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, b),
+                                                  __builtin_bit_cast(f16x8, a), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<__bf16> {
+  static __device__ __forceinline__ f32x4 mma(u32x4 b, u32x4 a, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, b),
+                                                   __builtin_bit_cast(bf16x8, a), c, 0, 0, 0);
+  }
+};
+
+// 32x32x16 products, same operand convention: lane l supplies row (first
+// operand) or column (second operand) l%32 and eight k values of group l/32;
+// result register r of lane l is C[m = l%32][n = 8*(r/4) + 4*(l/32) + r%4].
+template <typename T> struct Mfma32;
+template <> struct Mfma32<_Float16> {
+  static __device__ __forceinline__ f32x16 mma(u32x4 b, u32x4 a, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, b),
+                                                  __builtin_bit_cast(f16x8, a), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma32<__bf16> {
+  static __device__ __forceinline__ f32x16 mma(u32x4 b, u32x4 a, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, b),
+                                                   __builtin_bit_cast(bf16x8, a), c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ f32x4 mma_f32(float b, float a, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(b, a, c, 0, 0, 0);
+}
+
+// fp32 -> storage type, round to nearest even (hardware conversions).
+template <typename T> __device__ __forceinline__ uint16_t to_bits(float x);
+template <> __device__ __forceinline__ uint16_t to_bits<_Float16>(float x) {
+  return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+template <> __device__ __forceinline__ uint16_t to_bits<__bf16>(float x) {
+  return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+template <typename T> __device__ __forceinline__ float from_bits(uint16_t b);
+template <> __device__ __forceinline__ float from_bits<_Float16>(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+template <> __device__ __forceinline__ float from_bits<__bf16>(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)to_bits<T>(lo) | ((uint32_t)to_bits<T>(hi) << 16);
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit lane packing.  perm(hi_src, lo_src, sel): byte i of the result is
+// byte sel[i] of the 8-byte value {hi_src:lo_src}.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pack_lo16(uint32_t x, uint32_t y) {  // {x.lo, y.lo}
+  return __builtin_amdgcn_perm(y, x, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t x, uint32_t y) {  // {x.hi, y.hi}
+  return __builtin_amdgcn_perm(y, x, 0x07060302u);
+}
+
+// Transpose an 8x8 block of 16-bit values held as r[row] = 8 elements of one
+// row (element 2j in the low half of dword j).  On return c[col] holds the 8
+// elements of column `col`, row 0 in the low half of dword 0.
+__device__ __forceinline__ void transpose8x8_b16(const u32x4 r[8], u32x4 c[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    // columns 2j (low halves) and 2j+1 (high halves) of dword j of each row
+    u32x4 lo, hi;
+    lo.x = pack_lo16(r[0][j], r[1][j]);
+    lo.y = pack_lo16(r[2][j], r[3][j]);
+    lo.z = pack_lo16(r[4][j], r[5][j]);
+    lo.w = pack_lo16(r[6][j], r[7][j]);
+    hi.x = pack_hi16(r[0][j], r[1][j]);
+    hi.y = pack_hi16(r[2][j], r[3][j]);
+    hi.z = pack_hi16(r[4][j], r[5][j]);
+    hi.w = pack_hi16(r[6][j], r[7][j]);
+    c[2 * j] = lo;
+    c[2 * j + 1] = hi;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LDS tile layout for 16-bit operands: rows of 64 k-values (128 bytes, eight
+// 16-byte chunks).  Rows are stored in pairs of 256 bytes (all 64 banks); the
+// 16 chunks of a pair are permuted so that
+//   * a 16-lane phase reading 16 consecutive rows at one chunk (an MFMA
+//     fragment read) hits 16 distinct 4-bank groups, and
+//   * a 16-lane phase writing chunks 0..7 of two rows, or chunk c of rows
+//     {n, n+8} for eight (c, n) pairs (the transposed B store), does too.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t lds_off128(int row, int chunk) {
+  const int p = row >> 1;
+  const int bg = ((((row & 1) ^ ((p >> 2) & 1))) << 3) | ((chunk ^ p) & 7);
+  return (uint32_t)(p * 256 + bg * 16);
+}
+
+// ---------------------------------------------------------------------------
+// Tile order.  The dispatcher hands workgroup w to XCD w % 8; consecutive
+// logical tiles are given to the same XCD so that its L2 sees a compact block
+// of A rows and B columns, and inside that order tiles are grouped
+// `group_m` rows at a time (column-major within the group).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void tile_coords(int wg, int tiles_m, int tiles_n, int group_m,
+                                            int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  const int xcd = wg & 7, local = wg >> 3;
+  const int base = total >> 3, rem = total & 7;
+  const int t = xcd * base + (xcd < rem ? xcd : rem) + local;
+  const int per_group = group_m * tiles_n;
+  const int g = t / per_group;
+  const int first_m = g * group_m;
+  const int gsz = (tiles_m - first_m) < group_m ? (tiles_m - first_m) : group_m;
+  const int r = t - g * per_group;
+  tm = first_m + r % gsz;
+  tn = r / gsz;
+}
+
+}  // namespace cmpext3

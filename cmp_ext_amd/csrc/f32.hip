@@ -1,0 +1,26 @@
+// Instantiations of the fp32 MFMA GEMM.
+#include "f32_kernel.h"
+#include "kernels.h"
+
+namespace cmpext3 {
+namespace {
+template <bool KN>
+hipError_t launch(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s) {
+  switch (id) {
+    case kF32Tile128:
+      hipLaunchKernelGGL((gemm_f32_kernel<KN, 128, 128>), grid, dim3(256), 0, s, p);
+      break;
+    case kF32Tile64:
+      hipLaunchKernelGGL((gemm_f32_kernel<KN, 64, 64>), grid, dim3(256), 0, s, p);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_f32(KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s) {
+  return lay == kKN ? launch<true>(id, p, grid, s) : launch<false>(id, p, grid, s);
+}
+}  // namespace cmpext3

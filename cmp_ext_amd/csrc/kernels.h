@@ -1,0 +1,17 @@
+// Launchers of the gfx950 GEMM kernels (one translation unit per family so
+// they build in parallel).  Each returns the hipError_t of its launch.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include "gemm_params.h"
+
+namespace cmpext3 {
+
+hipError_t launch_tile_f16(KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_tile_bf16(KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_skinny(DType dt, int mb, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_f32(KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_generic(DType dt, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
+
+}  // namespace cmpext3

@@ -1,0 +1,209 @@
+// pybind11 module `cmpext3` (built as cmp_ext_amd/_cmpext3*.so): the Python
+// surface of the MI355X GEMM library.  It mirrors the GEMM part of the
+// reference bindings (src/main.cpp:155-357, :1594-1602) and adds the three
+// dtype-specific matmul entry points.  Tensor checks and output allocation
+// happen here; every product goes through the C ABI (cmpext3_gemm_ex), which
+// launches the hand-written gfx950 kernels on PyTorch's current stream.
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/extension.h>
+
+#include <climits>
+#include <string>
+#include <vector>
+
+#include "../../include/cmpext3_gemm.h"
+
+namespace {
+
+int dtype_code(at::ScalarType t) {
+  switch (t) {
+    case at::kHalf: return CMPEXT3_F16;
+    case at::kBFloat16: return CMPEXT3_BF16;
+    case at::kFloat: return CMPEXT3_F32;
+    default: return -1;
+  }
+}
+
+void* current_stream(const torch::Tensor& t) {
+  return (void*)c10::hip::getCurrentHIPStream(t.get_device()).stream();
+}
+
+void check_status(int st, const char* op) {
+  TORCH_CHECK(st == CMPEXT3_OK, "cmpext3.", op, ": ", cmpext3_status_string(st));
+}
+
+int64_t checked_int(int64_t v, const char* what) {
+  TORCH_CHECK(v <= INT_MAX, what, " = ", v, " exceeds the supported range (2^31 - 1)");
+  return v;
+}
+
+// A 2-D operand usable as row-major with unit inner stride: returns the row
+// pitch, or -1 if a copy is needed.
+int64_t row_pitch(const torch::Tensor& t) {
+  const int64_t rows = t.size(0), cols = t.size(1);
+  if (cols > 1 && t.stride(1) != 1) return -1;
+  if (rows <= 1) return std::max<int64_t>(cols, 1);
+  if (t.stride(0) < std::max<int64_t>(cols, 1)) return -1;
+  return t.stride(0);
+}
+
+// C = A[M,K] * B[K,N].  B may also be a transposed view of a row-major
+// [N,K] tensor (e.g. W.t()), which is consumed in place with the NK layout.
+torch::Tensor matmul_impl(const torch::Tensor& a_in, const torch::Tensor& b_in, at::ScalarType want,
+                          const char* op) {
+  TORCH_CHECK(a_in.dim() == 2 && b_in.dim() == 2, "cmpext3.", op, ": expected 2-D tensors, got ",
+              a_in.dim(), "-D and ", b_in.dim(), "-D");
+  TORCH_CHECK(a_in.scalar_type() == want && b_in.scalar_type() == want, "cmpext3.", op, ": expected ",
+              c10::toString(want), " tensors, got ", a_in.scalar_type(), " and ", b_in.scalar_type());
+  TORCH_CHECK(a_in.size(1) == b_in.size(0), "cmpext3.", op, ": shape mismatch ", a_in.sizes(), " x ",
+              b_in.sizes());
+  TORCH_CHECK(a_in.is_cuda() && b_in.is_cuda(), "cmpext3.", op, ": tensors must be on a GPU");
+  TORCH_CHECK(a_in.device() == b_in.device(), "cmpext3.", op, ": device mismatch");
+  const int64_t M = checked_int(a_in.size(0), "M"), K = checked_int(a_in.size(1), "K"),
+                N = checked_int(b_in.size(1), "N");
+  c10::DeviceGuard guard(a_in.device());
+  torch::Tensor a = a_in;
+  int64_t lda = row_pitch(a);
+  if (lda < 0) {
+    a = a.contiguous();
+    lda = std::max<int64_t>(K, 1);
+  }
+  torch::Tensor b = b_in;
+  int layout = CMPEXT3_B_KN;
+  int64_t ldb = row_pitch(b);
+  if (ldb < 0) {
+    const torch::Tensor bt = b.t();  // [N, K]
+    const int64_t pt = row_pitch(bt);
+    if (pt >= 0) {
+      layout = CMPEXT3_B_NK;
+      ldb = pt;
+    } else {
+      b = b.contiguous();
+      ldb = std::max<int64_t>(N, 1);
+    }
+  }
+  torch::Tensor c = torch::empty({M, N}, a.options());
+  const int st = cmpext3_gemm_ex(dtype_code(want), layout, a.data_ptr(), lda, 0, b.data_ptr(), ldb, 0,
+                                 c.data_ptr(), std::max<int64_t>(N, 1), 0, nullptr, (int)M, (int)N, (int)K,
+                                 1, current_stream(a));
+  check_status(st, op);
+  return c;
+}
+
+torch::Tensor fp16_matmul(const torch::Tensor& a, const torch::Tensor& b) {
+  return matmul_impl(a, b, at::kHalf, "fp16_matmul");
+}
+torch::Tensor bf16_matmul(const torch::Tensor& a, const torch::Tensor& b) {
+  return matmul_impl(a, b, at::kBFloat16, "bf16_matmul");
+}
+torch::Tensor fp32_matmul(const torch::Tensor& a, const torch::Tensor& b) {
+  return matmul_impl(a, b, at::kFloat, "fp32_matmul");
+}
+
+// linear(input[..., K], weight[N, K], bias[N]) -> [..., N]
+// Reference: custom_linear_forward, src/main.cpp:155-256.  The weight is read
+// in place ([N,K] layout) instead of being transposed into a copy (:182), and
+// the bias is added in the GEMM epilogue instead of a second kernel (:229-246).
+torch::Tensor linear(torch::Tensor input, const torch::Tensor& weight, c10::optional<torch::Tensor> bias) {
+  TORCH_CHECK(input.dim() >= 2, "Input dim >= 2");
+  TORCH_CHECK(weight.dim() == 2, "Weight dim == 2");
+  TORCH_CHECK(input.device() == weight.device(), "Device mismatch");
+  TORCH_CHECK(input.scalar_type() == weight.scalar_type(), "Dtype mismatch");
+  const int code = dtype_code(input.scalar_type());
+  TORCH_CHECK(code >= 0, "Unsupported dtype");
+  const int64_t N = weight.size(0), K = weight.size(1);
+  TORCH_CHECK(input.size(-1) == K, "Input shape mismatch with Weight");
+  TORCH_CHECK(input.is_cuda(), "cmpext3.linear: tensors must be on a GPU");
+  c10::DeviceGuard guard(input.device());
+  input = input.contiguous();
+  const torch::Tensor w = weight.contiguous();
+  int64_t M = 1;
+  for (int64_t d = 0; d + 1 < input.dim(); ++d) M *= input.size(d);
+  checked_int(M, "M");
+  checked_int(N, "N");
+  checked_int(K, "K");
+  const void* bias_ptr = nullptr;
+  torch::Tensor bias_c;
+  if (bias.has_value() && bias->defined()) {
+    bias_c = *bias;
+    TORCH_CHECK(bias_c.device() == input.device(), "Bias device mismatch");
+    TORCH_CHECK(bias_c.scalar_type() == input.scalar_type(), "Bias dtype mismatch");
+    TORCH_CHECK(bias_c.dim() == 1, "Bias must be 1D");
+    TORCH_CHECK(bias_c.size(0) == N, "Bias size mismatch");
+    bias_c = bias_c.contiguous();
+    bias_ptr = bias_c.data_ptr();
+  }
+  std::vector<int64_t> out_shape(input.sizes().begin(), input.sizes().end() - 1);
+  out_shape.push_back(N);
+  torch::Tensor out = torch::empty(out_shape, input.options());
+  const int st = cmpext3_gemm_ex(code, CMPEXT3_B_NK, input.data_ptr(), std::max<int64_t>(K, 1), 0,
+                                 w.data_ptr(), std::max<int64_t>(K, 1), 0, out.data_ptr(),
+                                 std::max<int64_t>(N, 1), 0, bias_ptr, (int)M, (int)N, (int)K, 1,
+                                 current_stream(input));
+  check_status(st, "linear");
+  return out;
+}
+
+// bmm(input[B, M, K], mat2[B, K, N]) -> [B, M, N]
+// Reference: custom_bmm_forward, src/main.cpp:273-357, which launches one
+// GEMM per batch entry from a host loop (:313-351); here it is one launch.
+torch::Tensor bmm(torch::Tensor input, torch::Tensor mat2) {
+  TORCH_CHECK(input.dim() == 3, "Input must be 3D (B, M, K)");
+  TORCH_CHECK(mat2.dim() == 3, "Mat2 must be 3D (B, K, N)");
+  TORCH_CHECK(input.device() == mat2.device(), "Device mismatch");
+  TORCH_CHECK(input.dtype() == mat2.dtype(), "Dtype mismatch");
+  const int code = dtype_code(input.scalar_type());
+  TORCH_CHECK(code >= 0, "Unsupported dtype for custom bmm");
+  const int64_t Bn = input.size(0), M = input.size(1), K = input.size(2);
+  const int64_t N = mat2.size(2);
+  TORCH_CHECK(Bn == mat2.size(0), "Batch size mismatch");
+  TORCH_CHECK(K == mat2.size(1), "Contracting dimension (K) mismatch");
+  TORCH_CHECK(input.is_cuda(), "cmpext3.bmm: tensors must be on a GPU");
+  checked_int(Bn, "batch");
+  checked_int(M, "M");
+  checked_int(N, "N");
+  checked_int(K, "K");
+  c10::DeviceGuard guard(input.device());
+  input = input.contiguous();
+  mat2 = mat2.contiguous();
+  torch::Tensor out = torch::empty({Bn, M, N}, input.options());
+  const int st = cmpext3_gemm_ex(code, CMPEXT3_B_KN, input.data_ptr(), std::max<int64_t>(K, 1), M * K,
+                                 mat2.data_ptr(), std::max<int64_t>(N, 1), K * N, out.data_ptr(),
+                                 std::max<int64_t>(N, 1), M * N, nullptr, (int)M, (int)N, (int)K, (int)Bn,
+                                 current_stream(input));
+  check_status(st, "bmm");
+  return out;
+}
+
+std::string plan(const std::string& dtype, int64_t M, int64_t N, int64_t K, const std::string& layout,
+                 int64_t batch, bool has_bias) {
+  int code = dtype == "f16" || dtype == "fp16" ? CMPEXT3_F16
+             : dtype == "bf16"                  ? CMPEXT3_BF16
+             : dtype == "f32" || dtype == "fp32" ? CMPEXT3_F32
+                                                : -1;
+  const int lay = layout == "NK" ? CMPEXT3_B_NK : CMPEXT3_B_KN;
+  const int64_t ldb = lay == CMPEXT3_B_KN ? N : K;
+  char buf[256];
+  const int st = cmpext3_gemm_plan(code, lay, (int)M, (int)N, (int)K, std::max<int64_t>(K, 1),
+                                   std::max<int64_t>(ldb, 1), std::max<int64_t>(N, 1), 16, has_bias ? 1 : 0,
+                                   (int)batch, buf, sizeof buf);
+  TORCH_CHECK(st >= 0, "cmpext3.plan: ", cmpext3_status_string(st));
+  return std::string(buf);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_cmpext3, m) {
+  m.doc() = "cmpext3 dense GEMM operators for AMD Instinct MI355X (gfx950)";
+  m.def("fp16_matmul", &fp16_matmul, "C = A @ B for fp16 (fp32 accumulate)", py::arg("a"), py::arg("b"));
+  m.def("bf16_matmul", &bf16_matmul, "C = A @ B for bf16 (fp32 accumulate)", py::arg("a"), py::arg("b"));
+  m.def("fp32_matmul", &fp32_matmul, "C = A @ B for fp32", py::arg("a"), py::arg("b"));
+  m.def("linear", &linear, "Custom linear layer implementation", py::arg("input"), py::arg("weight"),
+        py::arg("bias") = py::none());
+  m.def("bmm", &bmm, "Custom Batch Matrix Multiplication", py::arg("input"), py::arg("mat2"));
+  m.def("plan", &plan, "Describe the kernel chosen for a GEMM shape", py::arg("dtype"), py::arg("M"),
+        py::arg("N"), py::arg("K"), py::arg("layout") = "KN", py::arg("batch") = 1,
+        py::arg("has_bias") = false);
+  m.def("version", []() { return std::string(cmpext3_version()); });
+}

@@ -1,0 +1,149 @@
+// Host-side kernel selector: argument validation, kernel choice and launch
+// geometry for every GEMM request.  The reference fixes one tile per dtype
+// at compile time (src/cuda/fp16_matmul.cu:12-22, bf16_matmul.cu:11-21,
+// fp32_matmul.cu:10-14); here the choice depends on dtype, M/N/K, layout and
+// alignment.
+#include "selector.h"
+
+#include <stdio.h>
+
+#include <algorithm>
+
+#include "../../include/cmpext3_gemm.h"
+
+namespace cmpext3 {
+namespace {
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+struct Candidate {
+  KernelId id;
+  int bm, bn;
+  int occupancy;  // workgroups resident per CU
+  double eff;     // relative per-flop efficiency of the tile
+};
+
+// Modelled cost of running `tiles` tiles of bm x bn: whole rounds of
+// kNumCUs * occupancy workgroups, each round taking occupancy * bm * bn / eff.
+double tile_cost(const Candidate& c, int64_t M, int64_t N, int64_t batch) {
+  const int64_t tiles = cdiv(M, c.bm) * cdiv(N, c.bn) * batch;
+  const int64_t slots = (int64_t)kNumCUs * c.occupancy;
+  const int64_t rounds = cdiv(tiles, slots);
+  return (double)rounds * c.occupancy * c.bm * c.bn / c.eff;
+}
+
+const Candidate* pick(const Candidate* c, int n, int64_t M, int64_t N, int64_t batch) {
+  const Candidate* best = &c[0];
+  double best_cost = tile_cost(c[0], M, N, batch);
+  for (int i = 1; i < n; ++i) {
+    const double cost = tile_cost(c[i], M, N, batch);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = &c[i];
+    }
+  }
+  return best;
+}
+
+const Candidate kTiles16[] = {
+    {kTile256x256, 256, 256, 1, 1.00},
+    {kTile256x224, 256, 224, 1, 0.98},
+    {kTile128x128, 128, 128, 2, 0.80},
+};
+const Candidate kTiles32[] = {
+    {kF32Tile128, 128, 128, 3, 1.00},
+    {kF32Tile64, 64, 64, 6, 0.85},
+};
+
+const char* kernel_name(KernelId id) {
+  switch (id) {
+    case kTile256x256: return "tile256x256";
+    case kTile256x224: return "tile256x224";
+    case kTile128x128: return "tile128x128";
+    case kSkinny: return "skinny";
+    case kF32Tile128: return "f32tile128x128";
+    case kF32Tile64: return "f32tile64x64";
+    case kGeneric16: return "generic64x64";
+    default: return "?";
+  }
+}
+
+}  // namespace
+
+int make_plan(const Request& r, Plan* plan) {
+  if (r.dtype != kF16 && r.dtype != kBF16 && r.dtype != kF32) return CMPEXT3_ERR_UNSUPPORTED;
+  if (r.layout != kKN && r.layout != kNK) return CMPEXT3_ERR_UNSUPPORTED;
+  if (r.M < 0 || r.N < 0 || r.K < 0 || r.batch < 0) return CMPEXT3_ERR_INVALID_ARG;
+  const int64_t kIntMax = 0x7FFFFFFF;
+  if (r.M > kIntMax || r.N > kIntMax || r.K > kIntMax) return CMPEXT3_ERR_TOO_LARGE;
+  const int64_t b_cols = r.layout == kKN ? r.N : r.K;
+  if (r.lda < std::max<int64_t>(1, r.K) || r.ldb < std::max<int64_t>(1, b_cols) ||
+      r.ldc < std::max<int64_t>(1, r.N))
+    return CMPEXT3_ERR_INVALID_ARG;
+  if (r.batch > 1 && (r.stride_a < 0 || r.stride_b < 0 || r.stride_c < 0)) return CMPEXT3_ERR_INVALID_ARG;
+  const int64_t esz = r.dtype == kF32 ? 4 : 2;
+  // Kernels address at most 256 rows of an operand from a per-tile base with
+  // 32-bit byte offsets.
+  if (256 * r.lda * esz > kIntMax || 256 * r.ldb * esz > kIntMax) return CMPEXT3_ERR_TOO_LARGE;
+  if (cdiv(r.M, 64) * cdiv(r.N, 64) > kIntMax) return CMPEXT3_ERR_TOO_LARGE;
+
+  Plan p{};
+  p.group_m = 4;
+  p.threads = 256;
+  const bool batched = r.batch > 1;
+  if (r.dtype == kF32) {
+    const Candidate* c = pick(kTiles32, 2, r.M, r.N, r.batch);
+    p.kernel = c->id;
+    p.bm = c->bm;
+    p.bn = c->bn;
+  } else {
+    const bool skinny_ok = r.layout == kKN && r.M <= 64 && r.align >= 16 && r.K % 8 == 0 &&
+                           r.lda % 8 == 0 && r.N % 2 == 0 && r.ldb % 2 == 0 &&
+                           (!batched || (r.stride_a % 8 == 0 && r.stride_b % 2 == 0));
+    const bool fast = r.align >= 16 && r.K % 8 == 0 && r.lda % 8 == 0 && r.ldb % 8 == 0 &&
+                      r.ldc % 4 == 0 && (r.layout == kNK || r.N % 8 == 0) &&
+                      (!batched || (r.stride_a % 8 == 0 && r.stride_b % 8 == 0 && r.stride_c % 4 == 0));
+    if (skinny_ok) {
+      p.kernel = kSkinny;
+      p.mb = (int)std::max<int64_t>(1, cdiv(r.M, 16));
+      p.bm = 16 * p.mb;
+      p.bn = 32;
+      p.threads = 512;
+      p.k_per_wave = (int)(cdiv(cdiv(r.K, 8), 32) * 32);
+    } else if (fast) {
+      const Candidate* c = pick(kTiles16, 3, r.M, r.N, r.batch);
+      p.kernel = c->id;
+      p.bm = c->bm;
+      p.bn = c->bn;
+    } else {
+      p.kernel = kGeneric16;
+      p.bm = 64;
+      p.bn = 64;
+    }
+  }
+  if (p.kernel == kSkinny) {
+    p.tiles_m = 1;
+    p.tiles_n = (int)cdiv(r.N, 32);
+  } else {
+    p.tiles_m = (int)cdiv(r.M, p.bm);
+    p.tiles_n = (int)cdiv(r.N, p.bn);
+  }
+  *plan = p;
+  return CMPEXT3_OK;
+}
+
+std::string describe(const Request& r, const Plan& p) {
+  static const char* dt[] = {"f16", "bf16", "f32"};
+  char buf[256];
+  snprintf(buf, sizeof buf, "kernel=%s dtype=%s layout=%s tile=%dx%d grid=%dx%dx%lld threads=%d",
+           kernel_name(p.kernel), dt[r.dtype], r.layout == kKN ? "KN" : "NK", p.bm, p.bn, p.tiles_m,
+           p.tiles_n, (long long)r.batch, p.threads);
+  std::string s(buf);
+  if (p.kernel == kSkinny) {
+    snprintf(buf, sizeof buf, " mb=%d k_per_wave=%d", p.mb, p.k_per_wave);
+    s += buf;
+  }
+  return s;
+}
+
+}  // namespace cmpext3

@@ -1,0 +1,105 @@
+/*
+ * cmpext3_gemm.h -- C ABI of the MI355X (gfx950) dense matrix-multiply library.
+ *
+ * Every entry point computes C = A * B (optionally batched, optionally plus a
+ * broadcast bias row) with fp32 accumulation and writes C in the input dtype.
+ * Matrices are row-major.  All pointers are device pointers owned by the
+ * caller; the library never allocates, frees or synchronises.  Work is
+ * enqueued on `stream` (a hipStream_t; NULL means the null stream) and the call
+ * returns as soon as the kernels are queued.
+ *
+ * Return value: CMPEXT3_OK (0); a negative CMPEXT3_ERR_* for a rejected
+ * argument (nothing was launched); or a positive hipError_t from the launch.
+ * cmpext3_status_string() turns any of them into text.
+ *
+ * The reference library (eastmoe/cmp_ext, `cmpext3`) has no C ABI: its
+ * launchers are C++ functions with mangled names declared at
+ * src/main.cpp:12-14 and called from src/main.cpp:204-224 and :319-349.  The
+ * first three entry points below take their place one for one, with the same
+ * argument order and meaning, plus the stream the reference lacks (it always
+ * launches on stream 0, fp16_matmul.cu:315).
+ */
+#ifndef CMPEXT3_GEMM_H
+#define CMPEXT3_GEMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CMPEXT3_OK 0
+#define CMPEXT3_ERR_INVALID_ARG (-1)  /* null pointer, negative size, bad stride */
+#define CMPEXT3_ERR_UNSUPPORTED (-2)  /* unknown dtype / layout */
+#define CMPEXT3_ERR_TOO_LARGE (-3)    /* a size or stride does not fit the kernels' 32-bit offsets */
+
+/* Element types. */
+#define CMPEXT3_F16 0
+#define CMPEXT3_BF16 1
+#define CMPEXT3_F32 2
+
+/* Layout of the B operand. */
+#define CMPEXT3_B_KN 0 /* B is [K, N] row-major (matmul / bmm)            */
+#define CMPEXT3_B_NK 1 /* B is [N, K] row-major (a Linear weight, W^T is used) */
+
+/*
+ * C[M,N] = A[M,K] * B[K,N], fp16 in, fp32 accumulate, fp16 out.
+ * Replaces launch_matmul_fp16 (src/cuda/fp16_matmul.cu:301-340), whose strides
+ * are lda=K, ldb=N, ldc=N (fp16_matmul.cu:311-313).  Any M, N, K >= 0.
+ */
+int cmpext3_matmul_fp16(const void* A, const void* B, void* C, int M, int N, int K, void* stream);
+
+/*
+ * C[M,N] = A[M,K] * B[K,N], bf16 in, fp32 accumulate, bf16 out.
+ * Replaces launch_matmul_bf16 (src/cuda/bf16_matmul.cu:232-254).
+ */
+int cmpext3_matmul_bf16(const void* A, const void* B, void* C, int M, int N, int K, void* stream);
+
+/*
+ * C[M,N] = A[M,K] * B[K,N] in fp32 (fp32 MFMA, fused multiply-add).
+ * Replaces launch_matmul_fp32 (src/cuda/fp32_matmul.cu:236-265).
+ */
+int cmpext3_matmul_fp32(const float* A, const float* B, float* C, int M, int N, int K, void* stream);
+
+/*
+ * General form used by the Python bindings for matmul, linear and bmm:
+ *   for b in [0, batch):  C_b = A_b * op(B_b) (+ bias)
+ * with A_b = A + b*stride_a (elements), etc.; op(B) = B for CMPEXT3_B_KN and
+ * B^T for CMPEXT3_B_NK.  lda/ldb/ldc are row pitches in elements; bias is
+ * NULL or a length-N vector of the same dtype added to every row before the
+ * final rounding.
+ * Replaces the host loop of custom_bmm_forward (src/main.cpp:313-351: one
+ * launch per batch entry) with one launch, and the weight.t().contiguous()
+ * copy plus separate bias kernel of custom_linear_forward
+ * (src/main.cpp:182, :229-246) with the B_NK layout and a fused bias.
+ */
+int cmpext3_gemm_ex(int dtype, int b_layout,
+                    const void* A, int64_t lda, int64_t stride_a,
+                    const void* B, int64_t ldb, int64_t stride_b,
+                    void* C, int64_t ldc, int64_t stride_c,
+                    const void* bias,
+                    int M, int N, int K, int batch, void* stream);
+
+/*
+ * Kernel selection, host only (no GPU needed): writes a one-line description
+ * of the kernel cmpext3_gemm_ex would launch for these arguments into buf and
+ * returns the kernel id (>= 0) or a negative CMPEXT3_ERR_*.  `align` is the
+ * largest power of two (up to 16) dividing the byte address of every operand.
+ * No counterpart in the reference, whose tile choice is fixed at compile time
+ * (fp16_matmul.cu:12-22, bf16_matmul.cu:11-21, fp32_matmul.cu:10-14).
+ */
+int cmpext3_gemm_plan(int dtype, int b_layout, int M, int N, int K,
+                      int64_t lda, int64_t ldb, int64_t ldc, int align, int has_bias, int batch,
+                      char* buf, int buflen);
+
+/* Text for a status code returned by the entry points above. */
+const char* cmpext3_status_string(int status);
+
+/* Library version string. */
+const char* cmpext3_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CMPEXT3_GEMM_H */

@@ -1,0 +1,68 @@
+"""The C-ABI library loads on a machine without a GPU, exports every symbol
+include/cmpext3_gemm.h declares, and rejects bad arguments before launching."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from cmp_ext_amd import cabi
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "cmpext3_gemm.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cmpext3_\w+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    syms = declared_symbols()
+    for s in ["cmpext3_matmul_fp16", "cmpext3_matmul_bf16", "cmpext3_matmul_fp32", "cmpext3_gemm_ex",
+              "cmpext3_gemm_plan", "cmpext3_status_string", "cmpext3_version"]:
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(cabi.LIB_PATH)
+    for s in declared_symbols():
+        assert hasattr(lib, s), s
+    assert set(declared_symbols()) == set(cabi.SIGNATURES), "ctypes table out of sync with the header"
+
+
+def test_version_and_status_strings():
+    assert b"gfx950" in cabi.lib().cmpext3_version()
+    assert cabi.status_string(0) == "success"
+    for st in (cabi.ERR_INVALID_ARG, cabi.ERR_UNSUPPORTED, cabi.ERR_TOO_LARGE):
+        assert cabi.status_string(st) != "unknown status"
+    assert cabi.status_string(-99) == "unknown status"
+
+
+@pytest.mark.parametrize("kw,err", [
+    (dict(M=-1), cabi.ERR_INVALID_ARG),
+    (dict(dtype=9), cabi.ERR_UNSUPPORTED),
+    (dict(layout=5), cabi.ERR_UNSUPPORTED),
+    (dict(lda=1), cabi.ERR_INVALID_ARG),
+    (dict(A=None), cabi.ERR_INVALID_ARG),     # null operand with work to do
+    (dict(C=None), cabi.ERR_INVALID_ARG),
+])
+def test_gemm_ex_rejects_before_launch(kw, err):
+    args = dict(dtype=cabi.F16, layout=cabi.B_KN, A=0x1000, lda=64, stride_a=0, B=0x2000, ldb=64, stride_b=0,
+                C=0x3000, ldc=64, stride_c=0, bias=None, M=64, N=64, K=64, batch=1)
+    args.update(kw)
+    st = cabi.lib().cmpext3_gemm_ex(args["dtype"], args["layout"], args["A"], args["lda"], args["stride_a"],
+                                    args["B"], args["ldb"], args["stride_b"], args["C"], args["ldc"],
+                                    args["stride_c"], args["bias"], args["M"], args["N"], args["K"],
+                                    args["batch"], None)
+    assert st == err
+
+
+def test_empty_problems_launch_nothing():
+    lib = cabi.lib()
+    # M == 0, N == 0 or batch == 0: success without touching the (null) pointers or the GPU
+    assert lib.cmpext3_gemm_ex(cabi.F16, cabi.B_KN, None, 8, 0, None, 8, 0, None, 8, 0, None, 0, 8, 8, 1, None) == 0
+    assert lib.cmpext3_gemm_ex(cabi.F32, cabi.B_KN, None, 8, 0, None, 8, 0, None, 8, 0, None, 8, 0, 8, 1, None) == 0
+    assert lib.cmpext3_gemm_ex(cabi.BF16, cabi.B_NK, None, 8, 0, None, 8, 0, None, 8, 0, None, 8, 8, 8, 0, None) == 0
+    assert lib.cmpext3_matmul_fp16(None, None, None, 0, 0, 0, None) == 0

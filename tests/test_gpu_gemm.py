@@ -1,0 +1,293 @@
+"""GPU parity of the gfx950 GEMM kernels against the float64 CPU oracle.
+
+Every kernel family the selector can pick is exercised (the coverage test at
+the end checks that), through the Python binding (`cmpext3`) and through the
+C ABI (ctypes on libcmpext3_gemm.so).  Error bounds are the operator
+contract's relative Frobenius bounds: fp32 1e-5, fp16 2e-3, bf16 1e-2.
+
+The five benchmark configurations are checked at full size three ways:
+sampled rows against the float64 oracle, every element against a PyTorch fp32
+GEMM on the GPU (within the same bound), and the column/row sums of C against
+the exact (1^T A) B and A (B 1) in float64.
+"""
+import numpy as np
+import pytest
+import torch
+
+import cmpext3
+from cmp_ext_amd import cabi
+from oracle import gemm_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DT = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
+CODE = {"fp16": cabi.F16, "bf16": cabi.BF16, "fp32": cabi.F32}
+MATMUL = {"fp16": cmpext3.fp16_matmul, "bf16": cmpext3.bf16_matmul, "fp32": cmpext3.fp32_matmul}
+KERNEL_NAMES = ["tile256x256", "tile256x224", "tile128x128", "skinny", "f32tile128x128", "f32tile64x64",
+                "generic64x64"]
+SEEN_KERNELS = set()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    torch.cuda.init()
+
+
+def note_kernel(dtype, M, N, K, layout="KN", batch=1, has_bias=False, a=None, b=None):
+    desc = cmpext3.plan(dtype, M, N, K, layout=layout, batch=batch, has_bias=has_bias)
+    name = desc.split()[0].split("=")[1]
+    SEEN_KERNELS.add(name)
+    return name
+
+
+def err_vs_oracle(out, a, b, dtype, bias=None, layout="KN"):
+    return O.reference_check(out.cpu(), a.cpu(), b.cpu(), dtype, bias.cpu() if bias is not None else None, layout)
+
+
+def run_matmul(dtype, M, N, K, seed=0, dist="normal", scale=None):
+    scale = scale if scale is not None else 1.0 / max(1.0, np.sqrt(K))
+    a, b = O.make_inputs(dtype, M, N, K, dist, scale, seed)
+    ag, bg = a.cuda(), b.cuda()
+    out = MATMUL[dtype](ag, bg)
+    torch.cuda.synchronize()
+    assert out.shape == (M, N) and out.dtype == DT[dtype]
+    return a, b, out
+
+
+# ---------------------------------------------------------------- edge shapes
+GENERIC_SHAPES = [(1, 1, 1), (3, 5, 7), (65, 33, 17), (100, 7, 33), (129, 257, 65), (2, 300, 9)]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("M,N,K", GENERIC_SHAPES)
+def test_generic_ragged(dtype, M, N, K):
+    assert note_kernel(dtype, M, N, K) in ("generic64x64", "skinny")
+    a, b, out = run_matmul(dtype, M, N, K, seed=M + N + K)
+    assert err_vs_oracle(out, a, b, dtype) <= O.TOLERANCE[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("M,N,K,kernel", [
+    (512, 512, 512, "tile128x128"),
+    (300, 200, 72, "tile128x128"),       # M, N and K tails
+    (130, 8, 8, "tile128x128"),
+    (4000, 4088, 1000, "tile256x256"),   # ragged 256x256 tiles
+    (4000, 14000, 520, "tile256x224"),   # ragged 256x224 tiles
+])
+def test_tiled_shapes(dtype, M, N, K, kernel):
+    assert note_kernel(dtype, M, N, K) == kernel
+    a, b, out = run_matmul(dtype, M, N, K, seed=7)
+    if M * N * K > 2e9:  # keep the float64 oracle cheap: sampled rows + fp32 GPU reference
+        rows = torch.randperm(M, generator=torch.Generator().manual_seed(1))[:96].sort().values
+        e = O.rel_frobenius(O.to_f64(out.cpu()[rows]), O.matmul_f64(O.to_f64(a[rows]), O.to_f64(b)))
+        assert e <= O.TOLERANCE[dtype]
+        ref = torch.matmul(a.cuda().float(), b.cuda().float())
+        e2 = ((out.double() - ref.double()).norm() / ref.double().norm()).item()
+        assert e2 <= O.TOLERANCE[dtype]
+    else:
+        assert err_vs_oracle(out, a, b, dtype) <= O.TOLERANCE[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("M,N,K", [(1, 8192, 1024), (16, 256, 8192), (17, 200, 72), (33, 96, 40),
+                                   (64, 1024, 512), (5, 2, 8)])
+def test_skinny(dtype, M, N, K):
+    assert note_kernel(dtype, M, N, K) == "skinny"
+    a, b, out = run_matmul(dtype, M, N, K, seed=M)
+    assert err_vs_oracle(out, a, b, dtype) <= O.TOLERANCE[dtype]
+
+
+@pytest.mark.parametrize("M,N,K,kernel", [(512, 512, 512, "f32tile64x64"), (65, 47, 3, "f32tile64x64"),
+                                          (1, 1, 1, "f32tile64x64"), (6144, 8192, 64, "f32tile128x128"),
+                                          (257, 131, 129, "f32tile64x64")])
+def test_fp32(M, N, K, kernel):
+    assert note_kernel("fp32", M, N, K) == kernel
+    a, b, out = run_matmul("fp32", M, N, K, seed=3, dist="uniform")
+    assert err_vs_oracle(out, a, b, "fp32") <= O.TOLERANCE["fp32"]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_k_zero_and_empty(dtype):
+    a = torch.zeros(5, 0, dtype=DT[dtype], device="cuda")
+    b = torch.zeros(0, 8, dtype=DT[dtype], device="cuda")
+    out = MATMUL[dtype](a, b)
+    torch.cuda.synchronize()
+    assert out.shape == (5, 8) and not out.any()
+    out = MATMUL[dtype](torch.zeros(0, 4, dtype=DT[dtype], device="cuda"), torch.ones(4, 3, dtype=DT[dtype], device="cuda"))
+    assert out.shape == (0, 3)
+    w = torch.zeros(6, 0, dtype=DT[dtype], device="cuda")
+    bias = torch.arange(6, dtype=DT[dtype], device="cuda")
+    out = cmpext3.linear(torch.zeros(2, 3, 0, dtype=DT[dtype], device="cuda"), w, bias)
+    torch.cuda.synchronize()
+    assert out.shape == (2, 3, 6)
+    assert torch.equal(out, bias.expand(2, 3, 6))
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_exact_small_integers(dtype):
+    """Small-integer products are exact in every kernel: bit equality with the oracle."""
+    g = torch.Generator().manual_seed(5)
+    for M, N, K in [(300, 200, 72), (16, 64, 64), (7, 9, 11), (4096, 256, 64)]:
+        a = torch.randint(-3, 4, (M, K), generator=g).to(DT[dtype])
+        b = torch.randint(-3, 4, (K, N), generator=g).to(DT[dtype])
+        out = MATMUL[dtype](a.cuda(), b.cuda()).cpu()
+        ref = O.matmul_f64(O.to_f64(a), O.to_f64(b))
+        assert np.array_equal(O.to_f64(out), ref)
+
+
+def test_fp16_overflow_matches_rounding():
+    a = torch.full((4, 1), 300.0, dtype=torch.float16, device="cuda")
+    b = torch.full((1, 8), 300.0, dtype=torch.float16, device="cuda")
+    out = cmpext3.fp16_matmul(a, b).cpu()
+    assert torch.isinf(out).all()   # 90000 is beyond fp16's range, as in O.round_fp16
+
+
+# ------------------------------------------------------- layouts, views, bias
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("shape", [(2, 150, 72, 200), (1, 4096, 4096, 4096), (3, 7, 40, 12), (1, 16, 64, 64)])
+def test_linear_with_bias(dtype, shape):
+    Bt, S, K, N = shape
+    g = torch.Generator().manual_seed(sum(shape))
+    x = (torch.randn(Bt, S, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    w = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    bias = torch.randn(N, generator=g).to(DT[dtype])
+    out = cmpext3.linear(x.cuda(), w.cuda(), bias.cuda())
+    torch.cuda.synchronize()
+    assert out.shape == (Bt, S, N)
+    note_kernel(dtype, Bt * S, N, K, layout="NK", has_bias=True)
+    ref = O.linear_f64(O.to_f64(x), O.to_f64(w), O.to_f64(bias))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    out_nb = cmpext3.linear(x.cuda(), w.cuda())
+    assert O.rel_frobenius(O.to_f64(out_nb.cpu()), O.linear_f64(O.to_f64(x), O.to_f64(w))) <= O.TOLERANCE[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_views_and_layouts(dtype):
+    g = torch.Generator().manual_seed(9)
+    base = torch.randn(130, 97, generator=g).to(DT[dtype]).cuda()
+    w = torch.randn(64, 96, generator=g).to(DT[dtype]).cuda()
+    a = base[1:, 1:]                # offset view: misaligned rows and base pointer
+    bt = w.t()                      # [96, 64] transposed view -> consumed as NK
+    out = MATMUL[dtype](a, bt)
+    ref = O.matmul_f64(O.to_f64(a.cpu()), O.to_f64(bt.cpu()))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    a2 = base[:, ::2][:, :48]       # non-unit inner stride -> copied
+    b2 = torch.randn(48, 33, generator=g).to(DT[dtype]).cuda()
+    out2 = MATMUL[dtype](a2, b2)
+    ref2 = O.matmul_f64(O.to_f64(a2.cpu()), O.to_f64(b2.cpu()))
+    assert O.rel_frobenius(O.to_f64(out2.cpu()), ref2) <= O.TOLERANCE[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("Bn,M,N,K", [(3, 64, 96, 40), (4, 512, 512, 512), (2, 16, 256, 128), (5, 7, 9, 11)])
+def test_bmm(dtype, Bn, M, N, K):
+    g = torch.Generator().manual_seed(Bn * M)
+    a = (torch.randn(Bn, M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    b = (torch.randn(Bn, K, N, generator=g) / np.sqrt(K)).to(DT[dtype])
+    out = cmpext3.bmm(a.cuda(), b.cuda())
+    torch.cuda.synchronize()
+    note_kernel(dtype, M, N, K, batch=Bn)
+    ref = O.bmm_f64(O.to_f64(a), O.to_f64(b))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    for i in range(Bn):  # each batch entry equals the 2-D op on its slice, bit for bit
+        single = MATMUL[dtype](a[i].cuda(), b[i].cuda())
+        if cmpext3.plan(dtype, M, N, K) == cmpext3.plan(dtype, M, N, K, batch=Bn).replace(f"x{Bn} ", "x1 "):
+            assert torch.equal(single, out[i])
+
+
+# ------------------------------------------------------------ C ABI, streams
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_c_abi_matches_binding(dtype):
+    for M, N, K in [(300, 200, 72), (16, 512, 256), (33, 41, 17)]:
+        a, b = O.make_inputs(dtype, M, N, K, "normal", 0.1, M)
+        ag, bg = a.cuda(), b.cuda()
+        c = torch.empty(M, N, dtype=DT[dtype], device="cuda")
+        assert cabi.matmul(CODE[dtype], ag, bg, c, M, N, K) == cabi.OK
+        c2 = torch.empty_like(c)
+        st = cabi.gemm_ex(CODE[dtype], cabi.B_KN, ag, K, 0, bg, N, 0, c2, N, 0, None, M, N, K)
+        assert st == cabi.OK
+        torch.cuda.synchronize()
+        assert torch.equal(c, c2)
+        assert torch.equal(c, MATMUL[dtype](ag, bg))
+        assert err_vs_oracle(c, a, b, dtype) <= O.TOLERANCE[dtype]
+
+
+def test_runs_on_current_stream_and_is_deterministic():
+    a, b = O.make_inputs("fp16", 1024, 1024, 1024, "normal", 1 / 32, 0)
+    ag, bg = a.cuda(), b.cuda()
+    ref = cmpext3.fp16_matmul(ag, bg)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        outs = [cmpext3.fp16_matmul(ag, bg) for _ in range(3)]
+    s.synchronize()
+    for o in outs:
+        assert torch.equal(o, ref)
+
+
+# --------------------------------------------------------- benchmark configs
+def _full_config_check(name, via_cabi=False):
+    c = O.CONFIGS[name]
+    dtype, M, N, K = c["dtype"], c["M"], c["N"], c["K"]
+    a, b = O.make_inputs(dtype, M, N, K, c["dist"], c.get("scale", 1.0), 0)
+    ag, bg = a.cuda(), b.cuda()
+    note_kernel(dtype, M, N, K)
+    out = MATMUL[dtype](ag, bg)
+    if via_cabi:
+        c2 = torch.empty_like(out)
+        assert cabi.matmul(CODE[dtype], ag, bg, c2, M, N, K) == cabi.OK
+        torch.cuda.synchronize()
+        assert torch.equal(out, c2)
+    torch.cuda.synchronize()
+    tol = O.TOLERANCE[dtype]
+    out_c = out.cpu()
+    af, bf = O.to_f64(a), O.to_f64(b)
+    # (1) sampled rows (always the first and last) against the float64 oracle
+    gen = torch.Generator().manual_seed(2)
+    rows = sorted(set([0, M - 1] + torch.randint(0, M, (min(M, 64),), generator=gen).tolist()))
+    e_rows = O.rel_frobenius(O.to_f64(out_c[rows]), O.matmul_f64(af[rows], bf))
+    assert e_rows <= tol, e_rows
+    # (2) every element against a PyTorch fp32 GEMM on the GPU
+    ref = torch.matmul(ag.float(), bg.float())
+    e_full = ((out.double() - ref.double()).norm() / ref.double().norm()).item()
+    assert e_full <= tol, e_full
+    # (3) column and row sums against the exact (1^T A) B and A (B 1)
+    of = O.to_f64(out_c)
+    e_col = O.rel_frobenius(of.sum(axis=0), af.sum(axis=0) @ bf)
+    e_row = O.rel_frobenius(of.sum(axis=1), af @ bf.sum(axis=1))
+    assert e_col <= tol and e_row <= tol, (e_col, e_row)
+    return e_rows, e_full
+
+
+def test_cfg1_fp32_512_full_oracle():
+    c = O.CONFIGS["cfg1_fp32_512"]
+    a, b = O.make_inputs("fp32", 512, 512, 512, c["dist"], 1.0, 0)
+    out = cmpext3.fp32_matmul(a.cuda(), b.cuda())
+    assert err_vs_oracle(out, a, b, "fp32") <= O.TOLERANCE["fp32"]
+    _full_config_check("cfg1_fp32_512")
+
+
+def test_cfg2_fp16_4096():
+    _full_config_check("cfg2_fp16_4096", via_cabi=True)
+
+
+def test_cfg3_bf16_mlp():
+    _full_config_check("cfg3_bf16_mlp")
+
+
+def test_cfg4_fp16_skinny():
+    _full_config_check("cfg4_fp16_skinny", via_cabi=True)
+    c = O.CONFIGS["cfg4_fp16_skinny"]
+    a, b = O.make_inputs("fp16", 16, 8192, 8192, c["dist"], c["scale"], 0)
+    out = cmpext3.fp16_matmul(a.cuda(), b.cuda())
+    assert err_vs_oracle(out, a, b, "fp16") <= O.TOLERANCE["fp16"]   # full float64 oracle
+
+
+def test_cfg5_fp32_ragged():
+    _full_config_check("cfg5_fp32_ragged", via_cabi=True)
+
+
+def test_every_kernel_family_was_exercised():
+    missing = set(KERNEL_NAMES) - SEEN_KERNELS
+    assert not missing, f"kernels never selected by these tests: {missing}"

@@ -1,0 +1,74 @@
+"""Host-side kernel selection and argument validation (no GPU needed)."""
+import pytest
+
+from cmp_ext_amd import cabi
+
+K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC = range(7)
+
+
+@pytest.mark.parametrize("dtype,M,N,K,expect", [
+    (cabi.F32, 512, 512, 512, K_F32_64),          # cfg1: 64 tiles of 64x64 beat 16 of 128x128
+    (cabi.F16, 4096, 4096, 4096, K_TILE256),      # cfg2: 256 tiles = one per CU
+    (cabi.BF16, 4096, 14336, 4096, K_TILE224),    # cfg3: 1024 tiles = 4 full waves
+    (cabi.F16, 16, 8192, 8192, K_SKINNY),         # cfg4
+    (cabi.F32, 4097, 3001, 2049, K_F32_64),       # cfg5: ragged
+    (cabi.F16, 1024, 1024, 1024, K_TILE128),      # small: more tiles wanted
+    (cabi.BF16, 64, 4096, 4096, K_SKINNY),
+    (cabi.BF16, 65, 4096, 4096, K_TILE128),
+])
+def test_config_kernel_choice(dtype, M, N, K, expect):
+    kid, desc = cabi.plan(dtype, cabi.B_KN, M, N, K)
+    assert kid == expect, desc
+
+
+def test_skinny_parameters():
+    kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 16, 8192, 8192)
+    assert kid == K_SKINNY
+    assert "mb=1" in desc and "k_per_wave=1024" in desc and "grid=1x256x1" in desc
+    kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 33, 100, 72)
+    assert kid == K_SKINNY and "mb=3" in desc and "k_per_wave=32" in desc
+
+
+@pytest.mark.parametrize("M,N,K,layout,align,expect", [
+    (300, 7, 64, cabi.B_KN, 16, K_GENERIC),     # N % 8 != 0 with KN layout
+    (300, 12, 64, cabi.B_NK, 16, K_TILE128),    # NK layout needs only N % 4 (8-byte C rows)
+    (300, 7, 64, cabi.B_NK, 16, K_GENERIC),     # ... which N = 7 is not
+    (300, 64, 33, cabi.B_KN, 16, K_GENERIC),    # K % 8 != 0
+    (300, 64, 64, cabi.B_KN, 8, K_GENERIC),     # misaligned operand
+    (16, 63, 64, cabi.B_KN, 16, K_GENERIC),     # skinny needs even N
+    (16, 64, 60, cabi.B_KN, 16, K_GENERIC),     # skinny needs K % 8 == 0
+    (16, 64, 64, cabi.B_NK, 16, K_TILE128),     # skinny is KN only
+])
+def test_alignment_fallbacks(M, N, K, layout, align, expect):
+    kid, desc = cabi.plan(cabi.F16, layout, M, N, K, align=align)
+    assert kid == expect, desc
+
+
+def test_fp32_any_alignment():
+    kid, _ = cabi.plan(cabi.F32, cabi.B_KN, 4097, 3001, 2049, align=4)
+    assert kid in (K_F32_64, K_F32_128)
+
+
+@pytest.mark.parametrize("args,err", [
+    (dict(dtype=7), cabi.ERR_UNSUPPORTED),
+    (dict(layout=2), cabi.ERR_UNSUPPORTED),
+    (dict(M=-1), cabi.ERR_INVALID_ARG),
+    (dict(K=-5), cabi.ERR_INVALID_ARG),
+    (dict(lda=3), cabi.ERR_INVALID_ARG),          # lda < K
+    (dict(ldb=3), cabi.ERR_INVALID_ARG),          # ldb < N
+    (dict(ldc=3), cabi.ERR_INVALID_ARG),          # ldc < N
+    (dict(lda=1 << 30), cabi.ERR_TOO_LARGE),      # 256 rows no longer fit 32-bit offsets
+])
+def test_validation_errors(args, err):
+    base = dict(dtype=cabi.F16, layout=cabi.B_KN, M=64, N=64, K=64)
+    base.update(args)
+    kw = {k: base[k] for k in ("lda", "ldb", "ldc") if k in base}
+    kid, _ = cabi.plan(base["dtype"], base["layout"], base["M"], base["N"], base["K"], **kw)
+    assert kid == err
+    assert cabi.status_string(err) not in ("success", "unknown status")
+
+
+def test_zero_sizes_are_valid():
+    for M, N, K in [(0, 5, 5), (5, 0, 5), (5, 5, 0)]:
+        kid, _ = cabi.plan(cabi.F16, cabi.B_KN, M, N, K)
+        assert kid >= 0
