@@ -108,8 +108,16 @@ def time_gpu(name: str, steps: int, warmup: int) -> dict:
     return r
 
 
+def log(msg: str) -> None:
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
 def cpu_baseline(name: str, budget_s: float = 10.0) -> dict:
-    """The reference CPU path (torch.matmul on CPU) on the same workload."""
+    """The reference CPU path (torch.matmul on CPU) on a bounded sample of
+    the same workload: the first `rows` rows of A times all of B, with `rows`
+    grown from 8 until one call takes about a second (or A is exhausted), then
+    repeated for about `budget_s` seconds.  Throughput per row is the same as
+    for the full problem (every row of C costs 2*N*K flop and the same B)."""
     import platform
 
     import torch
@@ -118,15 +126,25 @@ def cpu_baseline(name: str, budget_s: float = 10.0) -> dict:
 
     c = CONFIGS[name]
     a, b = make_inputs(c["dtype"], c["M"], c["N"], c["K"], c["dist"], c.get("scale", 1.0), 0)
-    cpu_matmul(a, b)  # warm-up
+    rows = min(8, c["M"])
+    while True:
+        t0 = time.perf_counter()
+        cpu_matmul(a[:rows], b)
+        dt = time.perf_counter() - t0
+        log(f"cpu baseline probe: {rows} rows in {dt:.3f} s")
+        if dt > 1.0 or rows >= c["M"]:
+            break
+        rows = min(c["M"], rows * 4)
     times = []
     t_start = time.perf_counter()
     while (len(times) < 3 or time.perf_counter() - t_start < budget_s) and len(times) < 50:
         t0 = time.perf_counter()
-        cpu_matmul(a, b)
+        cpu_matmul(a[:rows], b)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    flops, nbytes = algorithmic(c)
+    esz = 4 if c["dtype"] == "fp32" else 2
+    flops = 2.0 * rows * c["N"] * c["K"]
+    nbytes = float(esz * (rows * c["K"] + c["K"] * c["N"] + rows * c["N"]))
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -137,11 +155,12 @@ def cpu_baseline(name: str, budget_s: float = 10.0) -> dict:
     except OSError:
         model = platform.processor()
     hbm = c.get("hbm")
-    return {"value": (nbytes / med / 1e9) if hbm else (flops / med / 1e12),
+    return {"value": round((nbytes / med / 1e9) if hbm else (flops / med / 1e12), 4),
             "unit": "GB/s" if hbm else "TFLOP/s",
             "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{c['desc']} via torch.matmul on CPU ({c['dtype']}), full size, median of {len(times)} "
-                      f"calls after 1 warm-up ({med * 1e3:.1f} ms/call); os.cpu_count()={os.cpu_count()}; {model}"}
+            "sample": f"torch.matmul on CPU ({c['dtype']}) of rows 0..{rows - 1} of A ({rows}x{c['K']}) "
+                      f"@ the full B ({c['K']}x{c['N']}) of {name}; median of {len(times)} calls "
+                      f"({med * 1e3:.1f} ms/call) after a warm-up; os.cpu_count()={os.cpu_count()}; {model}"}
 
 
 def load_traffic(name: str):
@@ -186,12 +205,16 @@ def main() -> int:
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    log(f"timing {args.config} ({args.warmup} warm-up + {args.steps} steps)")
     head = time_gpu(args.config, args.steps, args.warmup)
+    log(f"{args.config}: {head['ms_per_step']:.4f} ms/step, {head['tflops']:.1f} TFLOP/s, {head['gbs']:.0f} GB/s")
     others = {}
     if not args.no_others:
         for name in CONFIGS:
             if name != args.config:
+                log(f"timing {name}")
                 r = time_gpu(name, args.steps, args.warmup)
+                log(f"{name}: {r['ms_per_step']:.4f} ms/step, {r['tflops']:.1f} TFLOP/s, {r['gbs']:.0f} GB/s")
                 c = CONFIGS[name]
                 others[name] = {"desc": r["desc"], "kernel": r["kernel"], "ms_per_step": round(r["ms_per_step"], 5),
                                 **({"GB/s": round(r["gbs"], 1)} if c.get("hbm") else
@@ -217,6 +240,7 @@ def main() -> int:
         "roofline": roofline(head, args.config),
     }
     if not args.no_cpu:
+        log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(args.config)
     if others:
         line["other_configs"] = others
