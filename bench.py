@@ -193,6 +193,9 @@ def main() -> int:
     ap.add_argument("--config", default=HEADLINE, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-others", action="store_true", help="time only the headline workload")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="instead of GEMMs, run a plain device copy of MIB MiB per step (reference "
+                         "point for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the GEMM path has no multi-GPU "
@@ -205,6 +208,15 @@ def main() -> int:
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_per_step": n * 4, "steps": args.warmup + args.steps}))
+        return 0
     log(f"timing {args.config} ({args.warmup} warm-up + {args.steps} steps)")
     head = time_gpu(args.config, args.steps, args.warmup)
     log(f"{args.config}: {head['ms_per_step']:.4f} ms/step, {head['tflops']:.1f} TFLOP/s, {head['gbs']:.0f} GB/s")

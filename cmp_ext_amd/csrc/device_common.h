@@ -29,6 +29,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)kBufRecords, kBufWord3);
 }
 
+// LDS DMA of 16 bytes per lane: global (rsrc + voff) -> LDS (lds_addr +
+// 16 * lane), where lds_addr is wave-uniform and goes through M0.  Issued as
+// inline asm so that the compiler does not guard every later LDS read with a
+// wait for it: the kernels place their own "s_waitcnt vmcnt" fences (the
+// "memory" clobber keeps LDS accesses from moving across the issue point).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 make_rsrc_sgpr(const void* base) {
+  const uint64_t a = (uint64_t)base;
+  i32x4 r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)((a >> 32) & 0xFFFF);
+  r[2] = (int)kBufRecords;
+  r[3] = kBufWord3;
+  return r;
+}
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_load16(i32x4 rsrc, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(lds_addr)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(size_t)(__attribute__((address_space(3))) const void*)p;
+}
+
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }

@@ -6,59 +6,101 @@
 // stores), but built around the CDNA4 matrix cores instead of SIMT half2 FMAs,
 // and accumulating in fp32.
 //
-// Structure (one workgroup = one BM x BN output tile, WM x WN waves):
-//   * BK = 64.  A and B tiles are staged in LDS, two stages (double buffer),
-//     one barrier per K step.  Global loads for step k+1 are issued before the
-//     MFMAs of step k and written to LDS after them.
-//   * Global loads are 128-bit buffer loads; out-of-range chunks (rows >= M,
-//     columns >= N, k >= K) use an offset beyond the descriptor's range, so
-//     the hardware returns zeros without touching memory.
-//   * A [M,K] is K-contiguous and lands in LDS as is.  B [K,N] (matmul) is
-//     N-contiguous: each thread loads an 8(k) x 8(n) block, transposes it in
-//     registers (v_perm) and stores eight K-contiguous 16-byte rows, so both
-//     operands are read back with one ds_read_b128 per MFMA fragment.
-//     B [N,K] (a Linear weight) is already K-contiguous and is staged like A.
-//   * LDS rows are 128 bytes with the pair-swizzle of lds_off128(): fragment
-//     reads and all tile stores are free of bank conflicts.
-//   * Each wave owns a (BM/WM) x (BN/WN) block of 32x32 fp32 accumulators fed
-//     by v_mfma_f32_32x32x16_{f16,bf16}: per 16-deep k step a 128x128 wave
-//     tile reads 8 fragments (32 VGPRs) for 16 MFMAs.
+// Structure (one workgroup of 4 waves = one BM x BN output tile):
+//   * BK = 32.  Every operand tile goes global -> LDS by buffer_load_dwordx4
+//     ... lds (LDS DMA: no registers, no ds_write), into a ring of NS LDS
+//     stages.  The loads of K step t+NS-1 are issued while step t computes, so
+//     about NS-2 steps of matrix-core time cover the global-memory latency
+//     (a two-stage ring leaves the latency exposed on MI355X).
+//   * Step t+1 is certified (its DMA complete in every wave) at the barrier
+//     that ends step t-1, so the fragment reads for step t+1 are issued
+//     during step t, before that step's barrier: the barrier never waits on
+//     LDS latency.
+//   * A [M,K] and B [N,K] (the Linear-weight layout) are K-contiguous: LDS
+//     rows of 64 bytes (four 16-byte chunks), XOR-swizzled by row/4 so that a
+//     32x32x16 fragment read (16 rows per phase, one chunk) is conflict free.
+//     One ds_read_b128 per fragment.
+//   * B [K,N] (matmul) is N-contiguous: it stays [k][n] in LDS (64-byte
+//     segments XOR-swizzled by k%4) and each fragment is read with two
+//     ds_read_b64_tr_b16, the CDNA4 transposing LDS read: a 16-lane group
+//     pointing at a 4(k) x 16(n) block receives it transposed, lane i holding
+//     column i at 4 consecutive k.
+//   * Out-of-range chunks (rows >= M, columns >= N, k >= K) use an offset past
+//     the buffer descriptor's range: the hardware writes zeros into LDS and
+//     touches no memory.
+//   * Each wave owns a (BM/WM) x (BN/WN) block of 32x32 fp32 accumulators
+//     (AGPRs) fed by v_mfma_f32_32x32x16_{f16,bf16};
+//     __builtin_amdgcn_sched_group_barrier interleaves the DMA issue and the
+//     LDS reads with the MFMAs.
 #pragma once
 
 #include "device_common.h"
 
 namespace cmpext3 {
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, bool KN, int NS_>
 struct TileShape {
-  static constexpr int BK = 64;
+  static constexpr int BK = 32;
+  static constexpr int NS = NS_;
   static constexpr int NT = WM * WN * 64;
   static constexpr int WTM = BM / WM;
   static constexpr int WTN = BN / WN;
   static constexpr int FM = WTM / 32;  // 32x32 accumulator blocks per wave
   static constexpr int FN = WTN / 32;
-  static constexpr int A_BYTES = BM * 128;
-  static constexpr int B_BYTES = BN * 128;
+  static constexpr int A_BYTES = BM * 64;
+  static constexpr int B_PITCH = KN ? (BN * 2 + 255) / 256 * 256 : 64;  // bytes per LDS row of B
+  static constexpr int B_BYTES = KN ? BK * B_PITCH : (BN + 63) / 64 * 64 * 64;  // rows >= BN are OOB
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int LDS = 2 * STAGE;
-  static constexpr int A_LD = BM * 8 / NT;  // 16-byte A chunks per thread
-  static constexpr int B_LD = BN * 8 / NT;  // NK layout: 16-byte B chunks per thread
-  static constexpr int B_BLK = BN;  // KN layout: 8x8 blocks in a B stage (8 k-blocks x BN/8)
-  static constexpr int B_BLD = (B_BLK + NT - 1) / NT;
+  static constexpr int LDS = NS * STAGE;
+  static constexpr int A_DMA = A_BYTES / 1024 / 4;  // 1 KB LDS-DMA loads per wave per stage
+  static constexpr int B_DMA = B_BYTES / 1024 / 4;
+  static constexpr int DMA = A_DMA + B_DMA;
+  static_assert(NT == 256, "four waves");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
+  static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "whole DMA loads per wave");
+  static_assert(NS >= 3, "ring of at least three stages");
   static_assert(LDS <= 160 * 1024, "LDS budget");
-  static_assert(BM * 8 % NT == 0 && BN * 8 % NT == 0, "whole chunk rows per pass");
 };
 
-template <typename T, bool KN, int BM, int BN, int WM, int WN>
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSgMfma = 0x008, kSgDsRead = 0x100;
+
+// LDS byte offset of 16-byte chunk `chunk` (0..3) of row `row` in a tile of
+// 64-byte rows: groups of four rows fill one 256-byte bank line, chunks are
+// XORed with (row/4)%4, so 16 consecutive rows at one chunk hit 16 distinct
+// 4-bank groups.
+__device__ __forceinline__ uint32_t lds_off64(int row, int chunk) {
+  return (uint32_t)((row >> 2) * 256 + 16 * (4 * (row & 3) + (chunk ^ ((row >> 2) & 3))));
+}
+
+// Row and chunk that lane `lane` of 1 KB LDS-DMA load `slot` must fetch so
+// that LDS holds the lds_off64() layout (inverse of lds_off64 at byte
+// slot*1024 + 16*lane).
+__device__ __forceinline__ void dma64_geom(int slot, int lane, int& row, int& chunk) {
+  row = 16 * slot + 4 * (lane >> 4) + ((lane & 15) >> 2);
+  chunk = (lane & 3) ^ (lane >> 4);
+}
+
+// [k][n] layout of an N-contiguous B tile: rows of `pitch` bytes (a multiple
+// of 256), 64-byte segments XORed with k%4.  Lane `lane` of DMA load `slot`
+// fetches row k, columns n..n+7.
+__device__ __forceinline__ void dma_kn_geom(int slot, int lane, int pitch, int& k, int& n) {
+  const int pos = slot * 1024 + 16 * lane;
+  k = pos / pitch;
+  const int within = pos - k * pitch;
+  const int seg = (within >> 6) ^ (k & 3);
+  n = (seg * 64 + (within & 63)) >> 1;
+}
+
+template <typename T, bool KN, int BM, int BN, int WM, int WN, int NS>
 __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmParams p) {
-  using S = TileShape<BM, BN, WM, WN>;
-  constexpr int NT = S::NT, FM = S::FM, FN = S::FN;
+  using S = TileShape<BM, BN, WM, WN, KN, NS>;
+  constexpr int FM = S::FM, FN = S::FN;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[S::LDS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wm = wave / WN;
   const int wn = wave - wm * WN;
 
@@ -73,83 +115,79 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmPa
   const T* Bbase = KN ? (const T*)p.B + bz * p.stride_b + n0
                       : (const T*)p.B + bz * p.stride_b + (int64_t)n0 * ldb;
 
-  // ---- per-thread load descriptors, fixed for the whole K loop ----
-  // A (and NK-layout B) chunk loads: thread -> chunk c = tid%8 of rows
-  // tid/8 + (NT/8)*i.  Row r+NT/8 is (NT/16)*256 bytes further on in LDS.
-  constexpr int RSTEP = NT / 8;
-  static_assert(RSTEP % 16 == 0, "row step must keep the LDS swizzle phase");
-  const int ch = tid & 7;
-  const int crow = tid >> 3;
-  const uint32_t a_goff = (uint32_t)(crow * lda + 8 * ch) * (uint32_t)sizeof(T);
-  const uint32_t a_rstep = (uint32_t)(RSTEP * lda) * (uint32_t)sizeof(T);
-  const uint32_t c_soff = lds_off128(crow, ch);
-  const int a_rows = M - m0 - crow;  // row i is valid when RSTEP*i < a_rows
-  // KN-layout B: thread -> 8x8 block (k-block kc = tid%8, n-block nc = tid/8).
-  const int kc = tid & 7, nc = tid >> 3;
-  const bool b_blk = (S::B_BLK % NT == 0) || tid < S::B_BLK;
-  const bool b_col_ok = b_blk && (n0 + 8 * nc < N);
-  const uint32_t b_goff = KN ? (uint32_t)((8 * kc) * ldb + 8 * nc) * (uint32_t)sizeof(T)
-                             : (uint32_t)(crow * ldb + 8 * ch) * (uint32_t)sizeof(T);
-  const uint32_t b_rstep = (uint32_t)(RSTEP * ldb) * (uint32_t)sizeof(T);
-  const int b_rows = N - n0 - crow;
-  const uint32_t ldb_bytes = (uint32_t)(ldb * (int64_t)sizeof(T));
-  static_assert(!KN || S::B_BLD == 1, "KN layout: one 8x8 block per thread");
-
-  u32x4 ra[S::A_LD];
-  u32x4 rb[KN ? 8 : S::B_LD];
-
-  auto load_tile = [&](int k0) {
-    const __amdgpu_buffer_rsrc_t ra_rsrc = make_rsrc(Abase + k0);
-    const bool a_kok = k0 + 8 * ch < K;
+  // ---- per-lane DMA sources, fixed for the whole K loop ----
+  // offsets are relative to the step's first k; rows past the matrix are OOB
+  uint32_t a_off[S::A_DMA];
+  int a_kx[S::A_DMA];  // k offset of the lane's chunk within the step
 #pragma unroll
-    for (int i = 0; i < S::A_LD; ++i) {
-      const bool ok = a_kok && (RSTEP * i < a_rows);
-      ra[i] = buf_load16(ra_rsrc, ok ? a_goff + i * a_rstep : kBufOOB);
-    }
+  for (int i = 0; i < S::A_DMA; ++i) {
+    int row, chunk;
+    dma64_geom(wave * S::A_DMA + i, lane, row, chunk);
+    a_off[i] = (m0 + row < M) ? (uint32_t)(row * lda + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
+    a_kx[i] = 8 * chunk;
+  }
+  uint32_t b_off[S::B_DMA];
+  int b_kx[S::B_DMA];
+#pragma unroll
+  for (int i = 0; i < S::B_DMA; ++i) {
     if (KN) {
-      const __amdgpu_buffer_rsrc_t rb_rsrc = make_rsrc(Bbase + (int64_t)k0 * ldb);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const bool ok = b_col_ok && (k0 + 8 * kc + j < K);
-        rb[j] = buf_load16(rb_rsrc, ok ? b_goff + j * ldb_bytes : kBufOOB);
-      }
+      int k, n;
+      dma_kn_geom(wave * S::B_DMA + i, lane, S::B_PITCH, k, n);
+      const bool ok = n < BN && n0 + n < N;
+      b_off[i] = ok ? (uint32_t)(k * ldb + n) * (uint32_t)sizeof(T) : kBufOOB;
+      b_kx[i] = k;
     } else {
-      const __amdgpu_buffer_rsrc_t rb_rsrc = make_rsrc(Bbase + k0);
-#pragma unroll
-      for (int i = 0; i < S::B_LD; ++i) {
-        const bool ok = a_kok && (RSTEP * i < b_rows);
-        rb[i] = buf_load16(rb_rsrc, ok ? b_goff + i * b_rstep : kBufOOB);
-      }
+      int row, chunk;
+      dma64_geom(wave * S::B_DMA + i, lane, row, chunk);
+      b_off[i] = (row < BN && n0 + row < N) ? (uint32_t)(row * ldb + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
+      b_kx[i] = 8 * chunk;
+    }
+  }
+
+  // LDS-DMA load `d` (0 .. DMA-1; A pieces first, then B) of K step `kt`, into
+  // ring slot kt % NS.  Every k is checked against K, so steps at or past the
+  // end load zeros.
+  auto dma_piece = [&](int kt, int d) {
+    const int k0 = kt * S::BK;
+    const uint32_t sA = lds_addr(smem) + (uint32_t)((kt % NS) * S::STAGE);
+    const int krem = K - k0;
+    if (d < S::A_DMA) {
+      const int i = d;
+      dma_load16(make_rsrc_sgpr(Abase + k0), a_kx[i] < krem ? a_off[i] : kBufOOB,
+                 sA + (wave * S::A_DMA + i) * 1024);
+    } else {
+      const int i = d - S::A_DMA;
+      dma_load16(make_rsrc_sgpr(KN ? Bbase + (int64_t)k0 * ldb : Bbase + k0), b_kx[i] < krem ? b_off[i] : kBufOOB,
+                 sA + S::A_BYTES + (wave * S::B_DMA + i) * 1024);
     }
   };
-
-  auto store_tile = [&](int stage) {
-    unsigned char* sA = smem + stage * S::STAGE;
-    unsigned char* sB = sA + S::A_BYTES;
+  auto load_step = [&](int kt) {
 #pragma unroll
-    for (int i = 0; i < S::A_LD; ++i) *(u32x4*)(sA + c_soff + i * (RSTEP / 2) * 256) = ra[i];
-    if (KN) {
-      if (b_blk) {
-        u32x4 cols[8];
-        transpose8x8_b16(rb, cols);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) *(u32x4*)(sB + lds_off128(8 * nc + j, kc)) = cols[j];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < S::B_LD; ++i) *(u32x4*)(sB + c_soff + i * (RSTEP / 2) * 256) = rb[i];
-    }
+    for (int d = 0; d < S::DMA; ++d) dma_piece(kt, d);
+  };
+  // Wait until at most NS-3 steps' DMA are in flight (so every step up to
+  // the one two ahead has landed in this wave's share of LDS), then barrier:
+  // after it, that step is complete for the whole workgroup.
+  auto certify = [&]() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 3) * S::DMA) : "memory");
   };
 
-  // Fragment read offsets: row r32 of the wave's first 32-row block at chunk
-  // 2*ks + h (k16 step ks, lane half h); each further 32-row block is 4096
-  // bytes further on (the swizzle repeats every 16 rows).
+  // ---- fragment read addresses ----
   const int r32 = lane & 31, h = lane >> 5;
-  uint32_t fa_off[4], fb_off[4];
+  const uint32_t fa0 = lds_off64(wm * S::WTM + r32, h);  // sub-step ks: ^ (ks << 5)
+  uint32_t fb0[KN ? FN : 1];
+  if (KN) {
+    // transposing reads: lane (group G = lane/16, s = lane%16) points at row
+    // 8*(G/2) + s/4 (+ 4 for the second read, + 16 for sub-step 1), columns
+    // 32j + 16*(G%2) + 4*(s%4) of the wave's block.
+    const int G = lane >> 4, s = lane & 15;
+    const int k = 8 * (G >> 1) + (s >> 2);
+    const int seg0 = (wn * S::WTN) >> 5;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    fa_off[ks] = lds_off128(wm * S::WTM + r32, 2 * ks + h);
-    fb_off[ks] = lds_off128(wn * S::WTN + r32, 2 * ks + h);
+    for (int j = 0; j < FN; ++j)
+      fb0[j] = (uint32_t)(k * S::B_PITCH + (((seg0 + j) ^ (k & 3)) << 6) + 32 * (G & 1) + 8 * (s & 3));
+  } else {
+    fb0[0] = lds_off64(wn * S::WTN + r32, h);
   }
 
   f32x16 acc[FM][FN];
@@ -160,36 +198,76 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmPa
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  auto compute = [&](int stage) {
-    const unsigned char* sA = smem + stage * S::STAGE;
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  u32x4 fa[2][FM], fb[2][FN];
+  auto read_frags = [&](int kt, int ks, int buf) {
+    const unsigned char* sA = smem + (kt % NS) * S::STAGE;
     const unsigned char* sB = sA + S::A_BYTES;
+    const uint32_t xa = fa0 ^ (uint32_t)(ks << 5);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      u32x4 af[FM], bf[FN];
+    for (int i = 0; i < FM; ++i) fa[buf][i] = *(const u32x4*)(sA + xa + i * 2048);
+    if (KN) {
 #pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = *(const u32x4*)(sA + fa_off[ks] + i * 4096);
+      for (int j = 0; j < FN; ++j) {
+        const unsigned char* q = sB + fb0[j] + ks * 16 * S::B_PITCH;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(q));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(q + 4 * S::B_PITCH));
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+        fb[buf][j] = u32x4{l2.x, l2.y, h2.x, h2.y};
+      }
+    } else {
+      const uint32_t xb = fb0[0] ^ (uint32_t)(ks << 5);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bf[j] = *(const u32x4*)(sB + fb_off[ks] + j * 4096);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = Mfma32<T>::mma(bf[j], af[i], acc[i][j]);
+      for (int j = 0; j < FN; ++j) fb[buf][j] = *(const u32x4*)(sB + xb + j * 2048);
     }
   };
+  auto mfma_one = [&](int buf, int x) {
+    const int i = x / FN, j = x % FN;
+    acc[i][j] = Mfma32<T>::mma(fb[buf][j], fa[buf][i], acc[i][j]);
+  };
+  auto mfmas = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = Mfma32<T>::mma(fb[buf][j], fa[buf][i], acc[i][j]);
+  };
+  constexpr int RD = FM + (KN ? 2 : 1) * FN;  // LDS read instructions per sub-step
 
   const int nk = (K + S::BK - 1) / S::BK;
   if (nk > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int stage = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) load_tile((kt + 1) * S::BK);
-    compute(stage);
-    if (more) store_tile(stage ^ 1);
-    __syncthreads();
+    // prologue: steps 0 .. NS-2 in flight; steps 0 and 1 certified
+#pragma unroll
+    for (int t = 0; t < NS - 1; ++t) load_step(t);
+    certify();
+    read_frags(0, 0, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+      // sub-step 0 (fragments in buffer 0): read sub-step 1's fragments into
+      // buffer 1 up front, then issue step kt+NS-1's DMA pieces one per MFMA
+      // (each inline-asm DMA is a scheduling boundary, so source order holds)
+      read_frags(kt, 1, 1);
+#pragma unroll
+      for (int x = 0; x < FM * FN; ++x) {
+        mfma_one(0, x);
+        if (x < S::DMA) dma_piece(kt + NS - 1, x);
+      }
+      // sub-step 1 (buffer 1): step kt+1's first fragments into buffer 0
+      // (certified at the last barrier; after the last step this reads a
+      // stale slot, which is never used)
+      read_frags(kt + 1, 0, 0);
+      mfmas(1);
+#pragma unroll
+      for (int x = 0; x < FM * FN; ++x) {
+        __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+        if (2 * x + 2 <= RD)
+          __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+        else if (2 * x < RD)
+          __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      certify();  // step kt+2
+    }
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // no LDS DMA may outlive the workgroup
   }
 
   // ---- epilogue: register 4q..4q+3 of block (i, j) is C[m][n..n+3] with
