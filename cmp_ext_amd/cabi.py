@@ -25,8 +25,9 @@ SIGNATURES = {
     "cmpext3_matmul_bf16": (_i, [_p, _p, _p, _i, _i, _i, _p]),
     "cmpext3_matmul_fp32": (_i, [_p, _p, _p, _i, _i, _i, _p]),
     "cmpext3_gemm_ex": (_i, [_i, _i, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p,
-                             _i, _i, _i, _i, _p]),
-    "cmpext3_gemm_plan": (_i, [_i, _i, _i, _i, _i, _i64, _i64, _i64, _i, _i, _i, _cp, _i]),
+                             _i, _i, _i, _i, _p, _i64, _p]),
+    "cmpext3_gemm_workspace_size": (_i64, [_i, _i, _i, _i, _i, _i]),
+    "cmpext3_gemm_plan": (_i, [_i, _i, _i, _i, _i, _i64, _i64, _i64, _i, _i, _i, _i64, _cp, _i]),
     "cmpext3_status_string": (_cp, [_i]),
     "cmpext3_version": (_cp, []),
 }
@@ -54,14 +55,18 @@ def status_string(st: int) -> str:
 
 def plan(dtype: int, layout: int, M: int, N: int, K: int, lda: int | None = None,
          ldb: int | None = None, ldc: int | None = None, align: int = 16, has_bias: bool = False,
-         batch: int = 1) -> tuple[int, str]:
+         batch: int = 1, workspace_bytes: int = 0) -> tuple[int, str]:
     lda = max(K, 1) if lda is None else lda
     ldb = max(N if layout == B_KN else K, 1) if ldb is None else ldb
     ldc = max(N, 1) if ldc is None else ldc
     buf = ctypes.create_string_buffer(256)
     kid = lib().cmpext3_gemm_plan(dtype, layout, M, N, K, lda, ldb, ldc, align, int(has_bias), batch,
-                                  buf, 256)
+                                  workspace_bytes, buf, 256)
     return kid, buf.value.decode()
+
+
+def workspace_size(dtype: int, layout: int, M: int, N: int, K: int, batch: int = 1) -> int:
+    return lib().cmpext3_gemm_workspace_size(dtype, layout, M, N, K, batch)
 
 
 def _stream_handle(stream) -> int:
@@ -71,14 +76,18 @@ def _stream_handle(stream) -> int:
 
 
 def gemm_ex(dtype: int, layout: int, A, lda: int, stride_a: int, B, ldb: int, stride_b: int, C,
-            ldc: int, stride_c: int, bias, M: int, N: int, K: int, batch: int = 1, stream=None) -> int:
-    """Call cmpext3_gemm_ex with raw device pointers (ints) or tensors."""
+            ldc: int, stride_c: int, bias, M: int, N: int, K: int, batch: int = 1, workspace=None,
+            stream=None) -> int:
+    """Call cmpext3_gemm_ex with raw device pointers (ints) or tensors.
+    `workspace` is None or a device tensor (its byte size is passed)."""
     def ptr(x):
         if x is None:
             return None
         return x.data_ptr() if hasattr(x, "data_ptr") else int(x)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     return lib().cmpext3_gemm_ex(dtype, layout, ptr(A), lda, stride_a, ptr(B), ldb, stride_b, ptr(C),
-                                 ldc, stride_c, ptr(bias), M, N, K, batch, _stream_handle(stream))
+                                 ldc, stride_c, ptr(bias), M, N, K, batch, ptr(workspace), ws_bytes,
+                                 _stream_handle(stream))
 
 
 def matmul(dtype: int, A, B, C, M: int, N: int, K: int, stream=None) -> int:

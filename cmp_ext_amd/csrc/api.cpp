@@ -4,6 +4,8 @@
 #include <hip/hip_runtime_api.h>
 #include <string.h>
 
+#include <stdint.h>
+
 #include <algorithm>
 
 #include "../../include/cmpext3_gemm.h"
@@ -22,10 +24,16 @@ int align_of(const void* ptr) {
   return a;
 }
 
-hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p, dim3 grid,
+hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p, dim3 grid, void* ws,
                     hipStream_t s) {
   const BLayout lay = (BLayout)layout;
   switch (plan.kernel) {
+    case kSkinnyWide: {
+      hipError_t e = launch_skinny_wide((DType)dtype, plan.mb, p, (float*)ws, plan.splits, plan.ksplit, grid, s);
+      if (e == hipSuccess && plan.splits > 1)
+        e = launch_skinny_reduce((DType)dtype, p, (const float*)ws, plan.splits, (int)grid.z, s);
+      return e;
+    }
     case kTile256x256:
     case kTile256x224:
     case kTile128x128:
@@ -50,7 +58,7 @@ constexpr int64_t kMaxGridZ = 65535;
 extern "C" int cmpext3_gemm_ex(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride_a,
                                const void* B, int64_t ldb, int64_t stride_b, void* C, int64_t ldc,
                                int64_t stride_c, const void* bias, int M, int N, int K, int batch,
-                               void* stream) {
+                               void* workspace, int64_t workspace_bytes, void* stream) {
   Request r{};
   r.dtype = dtype;
   r.layout = b_layout;
@@ -66,6 +74,7 @@ extern "C" int cmpext3_gemm_ex(int dtype, int b_layout, const void* A, int64_t l
   r.align = std::min(std::min(align_of(A), align_of(B)), std::min(align_of(C), align_of(bias)));
   r.has_bias = bias != nullptr;
   r.batch = batch;
+  r.ws_bytes = (workspace != nullptr && align_of(workspace) >= 16) ? workspace_bytes : 0;
   Plan plan;
   const int st = make_plan(r, &plan);
   if (st != CMPEXT3_OK) return st;
@@ -87,7 +96,6 @@ extern "C" int cmpext3_gemm_ex(int dtype, int b_layout, const void* A, int64_t l
   p.tiles_m = plan.tiles_m;
   p.tiles_n = plan.tiles_n;
   p.group_m = plan.group_m;
-  p.k_per_wave = plan.k_per_wave;
   hipStream_t s = (hipStream_t)stream;
   for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridZ) {
     const int64_t nb = std::min<int64_t>(kMaxGridZ, batch - b0);
@@ -95,7 +103,7 @@ extern "C" int cmpext3_gemm_ex(int dtype, int b_layout, const void* A, int64_t l
     p.B = (const char*)B + b0 * stride_b * esz;
     p.C = (char*)C + b0 * stride_c * esz;
     const dim3 grid((unsigned)(plan.tiles_m * plan.tiles_n), 1, (unsigned)nb);
-    const hipError_t e = dispatch(plan, dtype, b_layout, p, grid, s);
+    const hipError_t e = dispatch(plan, dtype, b_layout, p, grid, workspace, s);
     if (e != hipSuccess) return (int)e;
   }
   return CMPEXT3_OK;
@@ -103,21 +111,22 @@ extern "C" int cmpext3_gemm_ex(int dtype, int b_layout, const void* A, int64_t l
 
 extern "C" int cmpext3_matmul_fp16(const void* A, const void* B, void* C, int M, int N, int K, void* stream) {
   return cmpext3_gemm_ex(CMPEXT3_F16, CMPEXT3_B_KN, A, K > 1 ? K : 1, 0, B, N > 1 ? N : 1, 0, C, N > 1 ? N : 1, 0,
-                         nullptr, M, N, K, 1, stream);
+                         nullptr, M, N, K, 1, nullptr, 0, stream);
 }
 
 extern "C" int cmpext3_matmul_bf16(const void* A, const void* B, void* C, int M, int N, int K, void* stream) {
   return cmpext3_gemm_ex(CMPEXT3_BF16, CMPEXT3_B_KN, A, K > 1 ? K : 1, 0, B, N > 1 ? N : 1, 0, C, N > 1 ? N : 1, 0,
-                         nullptr, M, N, K, 1, stream);
+                         nullptr, M, N, K, 1, nullptr, 0, stream);
 }
 
 extern "C" int cmpext3_matmul_fp32(const float* A, const float* B, float* C, int M, int N, int K, void* stream) {
   return cmpext3_gemm_ex(CMPEXT3_F32, CMPEXT3_B_KN, A, K > 1 ? K : 1, 0, B, N > 1 ? N : 1, 0, C, N > 1 ? N : 1, 0,
-                         nullptr, M, N, K, 1, stream);
+                         nullptr, M, N, K, 1, nullptr, 0, stream);
 }
 
-extern "C" int cmpext3_gemm_plan(int dtype, int b_layout, int M, int N, int K, int64_t lda, int64_t ldb,
-                                 int64_t ldc, int align, int has_bias, int batch, char* buf, int buflen) {
+namespace {
+Request plan_request(int dtype, int b_layout, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc, int align,
+                     int has_bias, int batch, int64_t ws_bytes) {
   Request r{};
   r.dtype = dtype;
   r.layout = b_layout;
@@ -133,6 +142,24 @@ extern "C" int cmpext3_gemm_plan(int dtype, int b_layout, int M, int N, int K, i
   r.align = align;
   r.has_bias = has_bias != 0;
   r.batch = batch;
+  r.ws_bytes = ws_bytes;
+  return r;
+}
+}  // namespace
+
+extern "C" int64_t cmpext3_gemm_workspace_size(int dtype, int b_layout, int M, int N, int K, int batch) {
+  const int64_t ldb = b_layout == CMPEXT3_B_KN ? N : K;
+  const Request r = plan_request(dtype, b_layout, M, N, K, K > 1 ? K : 1, ldb > 1 ? ldb : 1, N > 1 ? N : 1, 16, 0,
+                                 batch, INT64_MAX);
+  Plan plan;
+  const int st = make_plan(r, &plan);
+  return st == CMPEXT3_OK ? plan.ws_bytes : (int64_t)st;
+}
+
+extern "C" int cmpext3_gemm_plan(int dtype, int b_layout, int M, int N, int K, int64_t lda, int64_t ldb,
+                                 int64_t ldc, int align, int has_bias, int batch, int64_t workspace_bytes, char* buf,
+                                 int buflen) {
+  const Request r = plan_request(dtype, b_layout, M, N, K, lda, ldb, ldc, align, has_bias, batch, workspace_bytes);
   Plan plan;
   const int st = make_plan(r, &plan);
   if (st != CMPEXT3_OK) return st;

@@ -176,6 +176,16 @@ __device__ __forceinline__ uint32_t lds_off128(int row, int chunk) {
   return (uint32_t)(p * 256 + bg * 16);
 }
 
+// Row and chunk (relative to the tile's first row) of the 16-byte piece that
+// lane `lane` of 1 KB LDS-DMA load `slot` must fetch so that LDS ends up in
+// the lds_off128() layout (the inverse of lds_off128 at slot*1024 + 16*lane).
+__device__ __forceinline__ void dma128_geom(int slot, int lane, int& row, int& chunk) {
+  const int pp = 4 * slot + (lane >> 4);
+  const int bg = lane & 15;
+  row = 2 * pp + (((bg >> 3) ^ (pp >> 2)) & 1);
+  chunk = (bg & 7) ^ (pp & 7);
+}
+
 // ---------------------------------------------------------------------------
 // Tile order.  The dispatcher hands workgroup w to XCD w % 8; consecutive
 // logical tiles are given to the same XCD so that its L2 sees a compact block

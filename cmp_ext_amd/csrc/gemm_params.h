@@ -21,19 +21,19 @@ struct GemmParams {
   int M, N, K;
   int tiles_m, tiles_n;  // grid of output tiles (tiled kernels)
   int group_m;           // rows of tiles per ordering group
-  int k_per_wave;        // skinny kernel: K range of one wave (multiple of 32)
 };
 
 // Every kernel the library can launch.  The selector returns one of these.
 enum KernelId : int {
-  kTile256x256 = 0,   // f16/bf16 MFMA 16x16x32, 4 waves, 128x128 per wave
-  kTile256x224 = 1,   // same, 128x112 per wave (N tiles of 224)
-  kTile128x128 = 2,   // same, 64x64 per wave
-  kSkinny = 3,        // f16/bf16, M <= 64, B streamed once, K split over waves
+  kTile256x256 = 0,   // f16/bf16 MFMA 32x32x16, 4 waves of 128x128, LDS-DMA ring
+  kTile256x224 = 1,   // same, 4 waves of 64x224 (N tiles of 224)
+  kTile128x128 = 2,   // same, 4 waves of 64x64, two workgroups per CU
+  kSkinny = 3,        // f16/bf16, M <= 64: 32-column strips through an LDS-DMA ring
   kF32Tile128 = 4,    // fp32 MFMA 16x16x4, 128x128 tile
   kF32Tile64 = 5,     // fp32 MFMA 16x16x4, 64x64 tile
   kGeneric16 = 6,     // f16/bf16 any shape and alignment (element loads)
-  kNumKernels = 7
+  kSkinnyWide = 7,    // f16/bf16, M <= 64: 128-column strips, K split over workgroups
+  kNumKernels = 8
 };
 
 }  // namespace cmpext3

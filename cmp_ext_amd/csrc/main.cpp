@@ -38,6 +38,15 @@ int64_t checked_int(int64_t v, const char* what) {
   return v;
 }
 
+// Workspace for cmpext3_gemm_ex (the skinny-M path splits K into fp32
+// partials), from PyTorch's caching allocator on the operands' device.
+torch::Tensor workspace_for(int code, int layout, int64_t M, int64_t N, int64_t K, int64_t batch,
+                            const torch::Tensor& like) {
+  const int64_t bytes = cmpext3_gemm_workspace_size(code, layout, (int)M, (int)N, (int)K, (int)batch);
+  if (bytes <= 0) return torch::Tensor();
+  return torch::empty({bytes}, like.options().dtype(torch::kUInt8));
+}
+
 // A 2-D operand usable as row-major with unit inner stride: returns the row
 // pitch, or -1 if a copy is needed.
 int64_t row_pitch(const torch::Tensor& t) {
@@ -84,9 +93,11 @@ torch::Tensor matmul_impl(const torch::Tensor& a_in, const torch::Tensor& b_in, 
     }
   }
   torch::Tensor c = torch::empty({M, N}, a.options());
+  const torch::Tensor ws = workspace_for(dtype_code(want), layout, M, N, K, 1, a);
   const int st = cmpext3_gemm_ex(dtype_code(want), layout, a.data_ptr(), lda, 0, b.data_ptr(), ldb, 0,
                                  c.data_ptr(), std::max<int64_t>(N, 1), 0, nullptr, (int)M, (int)N, (int)K,
-                                 1, current_stream(a));
+                                 1, ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws.numel() : 0,
+                                 current_stream(a));
   check_status(st, op);
   return c;
 }
@@ -139,7 +150,7 @@ torch::Tensor linear(torch::Tensor input, const torch::Tensor& weight, c10::opti
   torch::Tensor out = torch::empty(out_shape, input.options());
   const int st = cmpext3_gemm_ex(code, CMPEXT3_B_NK, input.data_ptr(), std::max<int64_t>(K, 1), 0,
                                  w.data_ptr(), std::max<int64_t>(K, 1), 0, out.data_ptr(),
-                                 std::max<int64_t>(N, 1), 0, bias_ptr, (int)M, (int)N, (int)K, 1,
+                                 std::max<int64_t>(N, 1), 0, bias_ptr, (int)M, (int)N, (int)K, 1, nullptr, 0,
                                  current_stream(input));
   check_status(st, "linear");
   return out;
@@ -168,9 +179,11 @@ torch::Tensor bmm(torch::Tensor input, torch::Tensor mat2) {
   input = input.contiguous();
   mat2 = mat2.contiguous();
   torch::Tensor out = torch::empty({Bn, M, N}, input.options());
+  const torch::Tensor ws = workspace_for(code, CMPEXT3_B_KN, M, N, K, Bn, input);
   const int st = cmpext3_gemm_ex(code, CMPEXT3_B_KN, input.data_ptr(), std::max<int64_t>(K, 1), M * K,
                                  mat2.data_ptr(), std::max<int64_t>(N, 1), K * N, out.data_ptr(),
                                  std::max<int64_t>(N, 1), M * N, nullptr, (int)M, (int)N, (int)K, (int)Bn,
+                                 ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws.numel() : 0,
                                  current_stream(input));
   check_status(st, "bmm");
   return out;
@@ -185,9 +198,10 @@ std::string plan(const std::string& dtype, int64_t M, int64_t N, int64_t K, cons
   const int lay = layout == "NK" ? CMPEXT3_B_NK : CMPEXT3_B_KN;
   const int64_t ldb = lay == CMPEXT3_B_KN ? N : K;
   char buf[256];
+  // the bindings always provide the workspace a plan asks for
   const int st = cmpext3_gemm_plan(code, lay, (int)M, (int)N, (int)K, std::max<int64_t>(K, 1),
                                    std::max<int64_t>(ldb, 1), std::max<int64_t>(N, 1), 16, has_bias ? 1 : 0,
-                                   (int)batch, buf, sizeof buf);
+                                   (int)batch, INT64_MAX, buf, sizeof buf);
   TORCH_CHECK(st >= 0, "cmpext3.plan: ", cmpext3_status_string(st));
   return std::string(buf);
 }

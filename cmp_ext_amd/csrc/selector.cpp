@@ -61,6 +61,7 @@ const char* kernel_name(KernelId id) {
     case kTile256x224: return "tile256x224";
     case kTile128x128: return "tile128x128";
     case kSkinny: return "skinny";
+    case kSkinnyWide: return "skinny_wide";
     case kF32Tile128: return "f32tile128x128";
     case kF32Tile64: return "f32tile64x64";
     case kGeneric16: return "generic64x64";
@@ -98,18 +99,35 @@ int make_plan(const Request& r, Plan* plan) {
     p.bn = c->bn;
   } else {
     const bool skinny_ok = r.layout == kKN && r.M <= 64 && r.align >= 16 && r.K % 8 == 0 &&
-                           r.lda % 8 == 0 && r.N % 2 == 0 && r.ldb % 2 == 0 &&
-                           (!batched || (r.stride_a % 8 == 0 && r.stride_b % 2 == 0));
+                           r.lda % 8 == 0 && r.N % 8 == 0 && r.ldb % 8 == 0 &&
+                           (!batched || (r.stride_a % 8 == 0 && r.stride_b % 8 == 0));
     const bool fast = r.align >= 16 && r.K % 8 == 0 && r.lda % 8 == 0 && r.ldb % 8 == 0 &&
                       r.ldc % 4 == 0 && (r.layout == kNK || r.N % 8 == 0) &&
                       (!batched || (r.stride_a % 8 == 0 && r.stride_b % 8 == 0 && r.stride_c % 4 == 0));
     if (skinny_ok) {
-      p.kernel = kSkinny;
       p.mb = (int)std::max<int64_t>(1, cdiv(r.M, 16));
       p.bm = 16 * p.mb;
-      p.bn = 32;
-      p.threads = 512;
-      p.k_per_wave = (int)(cdiv(cdiv(r.K, 8), 32) * 32);
+      // Wide strips (128 columns: full 256-byte row segments, the faster HBM
+      // pattern) with K split over workgroups until ~256 of them exist; the
+      // splits need an fp32 workspace.  Narrow strips (32 columns, no split)
+      // when there is no workspace or the wide grid would be much smaller.
+      const int64_t chunk = std::min<int64_t>(r.batch, 65535);
+      const int64_t strips = cdiv(r.N, 128);
+      int64_t splits = 1;
+      if (strips * chunk < 192) splits = std::min<int64_t>(8, std::max<int64_t>(1, 256 / (strips * chunk)));
+      splits = std::min<int64_t>(splits, std::max<int64_t>(1, r.K / 256));
+      const int64_t need = splits > 1 ? splits * chunk * r.M * r.N * 4 : 0;
+      const int64_t wide_wgs = strips * splits * chunk, narrow_wgs = cdiv(r.N, 32) * chunk;
+      if (need <= r.ws_bytes && 2 * wide_wgs >= std::min<int64_t>(narrow_wgs, 256)) {
+        p.kernel = kSkinnyWide;
+        p.bn = 128;
+        p.splits = (int)splits;
+        p.ksplit = (int)(cdiv(cdiv(r.K, splits), 64) * 64);
+        p.ws_bytes = need;
+      } else {
+        p.kernel = kSkinny;
+        p.bn = 32;
+      }
     } else if (fast) {
       const Candidate* c = pick(kTiles16, 3, r.M, r.N, r.batch);
       p.kernel = c->id;
@@ -121,9 +139,10 @@ int make_plan(const Request& r, Plan* plan) {
       p.bn = 64;
     }
   }
-  if (p.kernel == kSkinny) {
+  if (p.splits == 0) p.splits = 1;
+  if (p.kernel == kSkinny || p.kernel == kSkinnyWide) {
     p.tiles_m = 1;
-    p.tiles_n = (int)cdiv(r.N, 32);
+    p.tiles_n = (int)cdiv(r.N, p.bn) * (p.kernel == kSkinnyWide ? p.splits : 1);
   } else {
     p.tiles_m = (int)cdiv(r.M, p.bm);
     p.tiles_n = (int)cdiv(r.N, p.bn);
@@ -139,8 +158,12 @@ std::string describe(const Request& r, const Plan& p) {
            kernel_name(p.kernel), dt[r.dtype], r.layout == kKN ? "KN" : "NK", p.bm, p.bn, p.tiles_m,
            p.tiles_n, (long long)r.batch, p.threads);
   std::string s(buf);
-  if (p.kernel == kSkinny) {
-    snprintf(buf, sizeof buf, " mb=%d k_per_wave=%d", p.mb, p.k_per_wave);
+  if (p.kernel == kSkinny || p.kernel == kSkinnyWide) {
+    snprintf(buf, sizeof buf, " mb=%d", p.mb);
+    s += buf;
+  }
+  if (p.kernel == kSkinnyWide) {
+    snprintf(buf, sizeof buf, " splits=%d ksplit=%d workspace=%lld", p.splits, p.ksplit, (long long)p.ws_bytes);
     s += buf;
   }
   return s;

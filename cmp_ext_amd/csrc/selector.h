@@ -16,8 +16,10 @@ struct Plan {
   int tiles_m, tiles_n;   // tile grid (skinny: tiles_m = 1, tiles_n = strips)
   int group_m;            // tile-order group height
   int mb;                 // skinny: 16-row blocks of M
-  int k_per_wave;         // skinny: K range per wave
   int threads;            // workgroup size
+  int splits;             // skinny wide: K splits (1 = no workspace)
+  int ksplit;             // skinny wide: K range per split (multiple of 64)
+  int64_t ws_bytes;       // workspace the plan needs
 };
 
 struct Request {
@@ -28,6 +30,7 @@ struct Request {
   int align;  // largest power of two (<= 16) dividing every operand address
   bool has_bias;
   int64_t batch;
+  int64_t ws_bytes;  // workspace the caller provides (0: none)
 };
 
 // Returns 0 and fills *plan, or a negative CMPEXT3_ERR_* code.

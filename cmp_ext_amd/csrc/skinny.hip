@@ -1,19 +1,18 @@
 // Instantiations of the skinny-M GEMM (M <= 64, B is [K, N]).
 #include "kernels.h"
 #include "skinny_kernel.h"
+#include "skinny_wide_kernel.h"
 
 namespace cmpext3 {
 namespace {
-constexpr int kPF = 4;  // K steps of loads in flight per wave
-
 template <typename T>
 hipError_t launch(int mb, const GemmParams& p, dim3 grid, hipStream_t s) {
-  const dim3 block(kSkinnyWaves * 64);
+  const dim3 block(256);
   switch (mb) {
-    case 1: hipLaunchKernelGGL((gemm_skinny_kernel<T, 1, kPF>), grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL((gemm_skinny_kernel<T, 2, kPF>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((gemm_skinny_kernel<T, 3, kPF>), grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL((gemm_skinny_kernel<T, 4, kPF>), grid, block, 0, s, p); break;
+    case 1: hipLaunchKernelGGL((gemm_skinny_narrow_kernel<T, 1>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((gemm_skinny_narrow_kernel<T, 2>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((gemm_skinny_narrow_kernel<T, 3>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((gemm_skinny_narrow_kernel<T, 4>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -24,5 +23,40 @@ hipError_t launch_skinny(DType dt, int mb, const GemmParams& p, dim3 grid, hipSt
   if (dt == kF16) return launch<_Float16>(mb, p, grid, s);
   if (dt == kBF16) return launch<__bf16>(mb, p, grid, s);
   return hipErrorInvalidValue;
+}
+
+namespace {
+template <typename T>
+hipError_t launch_wide(int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid, hipStream_t s) {
+  const dim3 block(256);
+  switch (mb) {
+    case 1: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 1>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    case 2: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 2>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    case 3: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 3>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    case 4: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 4>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_skinny_wide(DType dt, int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid,
+                              hipStream_t s) {
+  if (dt == kF16) return launch_wide<_Float16>(mb, p, ws, splits, ksplit, grid, s);
+  if (dt == kBF16) return launch_wide<__bf16>(mb, p, ws, splits, ksplit, grid, s);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_skinny_reduce(DType dt, const GemmParams& p, const float* ws, int splits, int batch,
+                                hipStream_t s) {
+  const int64_t quads = (int64_t)batch * p.M * (p.N / 4);
+  const dim3 grid((unsigned)((quads + 255) / 256));
+  if (dt == kF16)
+    hipLaunchKernelGGL((skinny_reduce_kernel<_Float16>), grid, dim3(256), 0, s, p, ws, splits, batch);
+  else if (dt == kBF16)
+    hipLaunchKernelGGL((skinny_reduce_kernel<__bf16>), grid, dim3(256), 0, s, p, ws, splits, batch);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 }  // namespace cmpext3

@@ -5,24 +5,43 @@
 // reference has no special path for them: its 128x128 tile kernel runs with
 // 112 of 128 rows zero-filled and only ceil(N/128) workgroups
 // (src/cuda/fp16_matmul.cu:318-321).  This kernel instead:
-//   * gives each workgroup a 32-column strip of B and all of K, so the number
-//     of workgroups is N/32 (256 for N = 8192: one per CU) and B is read
-//     exactly once, in full 64-byte row segments; strips are ordered so that
-//     neighbouring strips run on the same XCD;
-//   * splits K over the 8 waves of the workgroup and keeps PF steps of loads in
-//     flight per wave (each step: 32 k x 32 columns of B, 2 KB per wave);
-//   * feeds v_mfma_f32_16x16x32 directly from registers: lane (c, g) loads the
-//     32-bit pair B[k0+8g+i][2c..2c+1] for i = 0..7 and repacks it (v_perm)
-//     into the K-contiguous operands for columns 2c and 2c+1;
-//   * reduces the 8 per-wave partial sums in LDS and writes C once.
+//   * gives each workgroup (4 waves) a 32-column strip of B and all of K, so
+//     there are N/32 workgroups (256 for N = 8192: one per CU) and B is read
+//     exactly once; strips are ordered so that neighbouring strips (the two
+//     halves of each 128-byte line) run on the same XCD and share its L2;
+//   * streams the strip, and the matching A columns, global -> LDS with
+//     LDS-DMA (buffer_load_dwordx4 ... lds) through a ring of NS stages of KS
+//     k-rows, keeping NS-2 stages (tens of KB per CU) in flight to cover HBM
+//     latency without registers;
+//   * reads B fragments with ds_read_b64_tr_b16 (LDS keeps B as [k][n]) and A
+//     fragments with ds_read_b128 (A rows XOR-swizzled by row%16);
+//   * splits every stage's 32-deep k-blocks over the 4 waves
+//     (v_mfma_f32_16x16x32 with the M rows in the MFMA's 16-wide dimension)
+//     and reduces the 4 partial sums in LDS at the end.
 #pragma once
 
 #include "device_common.h"
 
 namespace cmpext3 {
 
-constexpr int kSkinnyWaves = 8;
-constexpr int kSkinnyStrip = 32;
+constexpr int kSkinnyStrip = 32;  // columns per workgroup
+
+template <int MB>
+struct SkinnyShape {
+  static constexpr int KS = MB <= 2 ? 256 : 128;  // k rows per stage
+  static constexpr int B_BYTES = KS * kSkinnyStrip * 2;
+  static constexpr int A_PITCH = KS * 2;           // bytes per A row in LDS
+  static constexpr int A_BYTES = MB * 16 * A_PITCH;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int NS = (160 * 1024) / STAGE > 8 ? 8 : (160 * 1024) / STAGE;
+  static constexpr int A_DMA = A_BYTES / 4096;  // 1 KB LDS-DMA loads per wave per stage
+  static constexpr int B_DMA = B_BYTES / 4096;
+  static constexpr int DMA = A_DMA + B_DMA;
+  static constexpr int KB = KS / 32 / 4;  // 32-deep k-blocks per wave per stage
+  static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "whole DMA loads per wave");
+  static_assert(NS >= 3 && (NS - 2) * DMA <= 63, "ring depth / vmcnt range");
+  static_assert(4 * MB * 16 * kSkinnyStrip * 4 <= NS * STAGE, "reduction fits the ring");
+};
 
 __device__ __forceinline__ int strip_order(int wg, int total) {
   const int xcd = wg & 7, local = wg >> 3;
@@ -30,110 +49,140 @@ __device__ __forceinline__ int strip_order(int wg, int total) {
   return xcd * base + (xcd < rem ? xcd : rem) + local;
 }
 
-template <typename T, int MB, int PF>
-__global__ void __launch_bounds__(kSkinnyWaves * 64) gemm_skinny_kernel(const GemmParams p) {
-  __shared__ float red[kSkinnyWaves][MB * 16][kSkinnyStrip + 1];
+// Byte offset in the B part of a stage of row k, 16-column half h (0/1):
+// rows are 64 bytes; the halves of rows with bit 3 of k set are swapped so
+// that a transposing read (rows k..k+3 and k+8..k+11 of one half) is
+// conflict free.
+__device__ __forceinline__ uint32_t skinny_off(int k, int h) {
+  return (uint32_t)(k * 64 + ((h ^ ((k >> 3) & 1)) << 5));
+}
+
+template <typename T, int MB>
+__global__ void __launch_bounds__(256) gemm_skinny_narrow_kernel(const GemmParams p) {
+  using S = SkinnyShape<MB>;
+  constexpr int NS = S::NS;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * S::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int c = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int strip = strip_order(blockIdx.x, gridDim.x);
   const int n0 = strip * kSkinnyStrip;
   const int M = p.M, N = p.N, K = p.K;
   const int64_t bz = blockIdx.z;
-  const int64_t ldb = p.ldb;
-
+  const int64_t lda = p.lda, ldb = p.ldb;
   const T* Ab = (const T*)p.A + bz * p.stride_a;
   const T* Bb = (const T*)p.B + bz * p.stride_b + n0;
-  const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(Ab);
 
-  const int kbeg = wave * p.k_per_wave;
-  const int kend = min(K, kbeg + p.k_per_wave);
-  const bool col_ok = n0 + 2 * c < N;  // N is even: the pair is in or out as a whole
-  const uint32_t ldb_bytes = (uint32_t)(ldb * (int64_t)sizeof(T));
-  const uint32_t b_lane = (uint32_t)(8 * g * ldb + 2 * c) * (uint32_t)sizeof(T);
-  uint32_t a_lane[MB];
-  bool a_row_ok[MB];
+  // ---- DMA sources (inverse of the LDS layouts), relative to the stage's k0 ----
+  uint32_t b_off[S::B_DMA];
+  int b_k[S::B_DMA];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int row = mb * 16 + c;
-    a_row_ok[mb] = row < M;
-    a_lane[mb] = (uint32_t)(row * p.lda + 8 * g) * (uint32_t)sizeof(T);
+  for (int i = 0; i < S::B_DMA; ++i) {
+    const int row = 16 * (wave * S::B_DMA + i) + (lane >> 2);  // 16 rows of 64 bytes per load
+    const int pos = 16 * (lane & 3);
+    const int h = (pos >> 5) ^ ((row >> 3) & 1);
+    const int col = h * 16 + ((pos & 31) >> 1);
+    b_off[i] = (n0 + col < N) ? (uint32_t)(row * ldb + col) * (uint32_t)sizeof(T) : kBufOOB;
+    b_k[i] = row;
   }
-
-  uint32_t bq[PF][8];
-  u32x4 aq[PF][MB];
-
-  auto load_step = [&](int s, int k) {
-    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(Bb + (int64_t)k * ldb);
+  uint32_t a_off[S::A_DMA];
+  int a_k[S::A_DMA];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const bool ok = col_ok && (k + 8 * g + i < kend);
-      bq[s][i] = buf_load4(b_rsrc, ok ? b_lane + i * ldb_bytes : kBufOOB);
-    }
+  for (int i = 0; i < S::A_DMA; ++i) {
+    const int pos = (wave * S::A_DMA + i) * 1024 + 16 * lane;
+    const int row = pos / S::A_PITCH;
+    const int chunk = ((pos % S::A_PITCH) >> 4) ^ (row & 15);
+    a_off[i] = (row < M) ? (uint32_t)(row * lda + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
+    a_k[i] = 8 * chunk;
+  }
+  auto load_stage = [&](int st) {
+    const int k0 = st * S::KS;
+    const uint32_t dst = lds_addr(smem) + (uint32_t)((st % NS) * S::STAGE);
+    const int krem = K - k0;
+    const i32x4 rb = make_rsrc_sgpr(Bb + (int64_t)k0 * ldb);
+    const i32x4 ra = make_rsrc_sgpr(Ab + k0);
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const bool ok = a_row_ok[mb] && (k + 8 * g < kend);
-      aq[s][mb] = buf_load16(a_rsrc, ok ? a_lane[mb] + (uint32_t)k * (uint32_t)sizeof(T) : kBufOOB);
-    }
+    for (int i = 0; i < S::B_DMA; ++i)
+      dma_load16(rb, b_k[i] < krem ? b_off[i] : kBufOOB, dst + (wave * S::B_DMA + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < S::A_DMA; ++i)
+      dma_load16(ra, a_k[i] < krem ? a_off[i] : kBufOOB, dst + S::B_BYTES + (wave * S::A_DMA + i) * 1024);
   };
 
-  f32x4 acc[MB][2];
+  // ---- fragments: lane (c = l%16, g = l/16) ----
+  // B (first MFMA operand): column nb + c at k = kb + 8g .. +7, two
+  //   transposing reads of source rows kb + 8g + 4r + c/4, columns 4*(c%4)..
+  // A (second operand): A[16*mb + c][kb + 8g .. +7]
+  const int c = lane & 15, g = lane >> 4;
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  f32x4 acc[2][MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    acc[mb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-    acc[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[h][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute_step = [&](int s) {
-    u32x4 b0, b1;  // K-contiguous operands of columns 2c and 2c+1
-    b0.x = pack_lo16(bq[s][0], bq[s][1]);
-    b0.y = pack_lo16(bq[s][2], bq[s][3]);
-    b0.z = pack_lo16(bq[s][4], bq[s][5]);
-    b0.w = pack_lo16(bq[s][6], bq[s][7]);
-    b1.x = pack_hi16(bq[s][0], bq[s][1]);
-    b1.y = pack_hi16(bq[s][2], bq[s][3]);
-    b1.z = pack_hi16(bq[s][4], bq[s][5]);
-    b1.w = pack_hi16(bq[s][6], bq[s][7]);
+  auto compute_stage = [&](int st) {
+    const unsigned char* stage = smem + (st % NS) * S::STAGE;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      acc[mb][0] = Mfma<T>::mma(b0, aq[s][mb], acc[mb][0]);
-      acc[mb][1] = Mfma<T>::mma(b1, aq[s][mb], acc[mb][1]);
-    }
-  };
-
-  if (kbeg < kend) {
+    for (int b = 0; b < S::KB; ++b) {
+      const int kb = (wave * S::KB + b) * 32;
+      u32x4 af[MB];
 #pragma unroll
-    for (int s = 0; s < PF; ++s) load_step(s, kbeg + 32 * s);
-    for (int k = kbeg; k < kend; k += 32 * PF) {
+      for (int mb = 0; mb < MB; ++mb)
+        af[mb] = *(const u32x4*)(stage + S::B_BYTES + (16 * mb + c) * S::A_PITCH + 16 * ((kb / 8 + g) ^ c));
 #pragma unroll
-      for (int s = 0; s < PF; ++s) {
-        compute_step(s);
-        load_step(s, k + 32 * (s + PF));
+      for (int h = 0; h < 2; ++h) {
+        u32x4 bf;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int k = kb + 8 * g + 4 * r + (c >> 2);
+          const unsigned char* q = stage + skinny_off(k, h) + 8 * (c & 3);
+          const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q);
+          const u32x2 v2 = __builtin_bit_cast(u32x2, v);
+          bf[2 * r] = v2.x;
+          bf[2 * r + 1] = v2.y;
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[h][mb] = Mfma<T>::mma(bf, af[mb], acc[h][mb]);
       }
     }
+  };
+
+  const int nst = (K + S::KS - 1) / S::KS;
+  // Step st: DMA stage st+NS-1 (zeros past K), compute st, then wait until at
+  // most NS-2 stages' DMA are in flight and barrier: stage st+1 is complete
+  // in LDS and stage st's slot may be refilled.
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t) load_stage(t);
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 2) * S::DMA) : "memory");
+  for (int st = 0; st < nst; ++st) {
+    load_stage(st + NS - 1);
+    compute_stage(st);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 2) * S::DMA) : "memory");
   }
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" : : : "memory");
 
-  // acc[mb][jj][r] = C[mb*16 + c][n0 + 2*(4g + r) + jj]
+  // ---- reduce the 4 waves' partial sums through LDS (the ring is free) ----
+  // acc[h][mb][r] = C[16*mb + c][n0 + 16*h + 4*g + r]
+  float* red = (float*)smem;  // [wave][MB*16][32]
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      red[wave][mb * 16 + c][2 * (4 * g + r)] = acc[mb][0][r];
-      red[wave][mb * 16 + c][2 * (4 * g + r) + 1] = acc[mb][1][r];
-    }
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        red[(wave * MB * 16 + 16 * mb + c) * kSkinnyStrip + 16 * h + 4 * g + r] = acc[h][mb][r];
   __syncthreads();
-
   T* Cb = (T*)p.C + bz * p.stride_c;
   const uint16_t* bias = (const uint16_t*)p.bias;
-  for (int o = tid; o < MB * 16 * kSkinnyStrip; o += kSkinnyWaves * 64) {
+  for (int o = tid; o < MB * 16 * kSkinnyStrip; o += 256) {
     const int row = o / kSkinnyStrip, col = o % kSkinnyStrip;
     const int n = n0 + col;
     if (row >= M || n >= N) continue;
     float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < kSkinnyWaves; ++w) s += red[w][row][col];
+    for (int w = 0; w < 4; ++w) s += red[(w * MB * 16 + row) * kSkinnyStrip + col];
     if (bias) s += from_bits<T>(bias[n]);
     ((uint16_t*)(Cb + (int64_t)row * p.ldc))[n] = to_bits<T>(s);
   }

@@ -1,0 +1,213 @@
+// Skinny-M f16/bf16 GEMM with split K (M <= 64, B is [K,N]), for callers that
+// provide a workspace: C = A * B (+ bias).
+//
+// HBM reads of 64-byte row segments (the 32-column strips of the narrow
+// skinny kernel) top out near 4 TB/s on MI355X; 256-byte segments reach
+// ~5.6 TB/s.  So here a workgroup owns a 128-column strip, and the K range is
+// split S ways across workgroups so that there are still ~256 of them
+// (16 x 8192 x 8192: 64 strips x 4 splits).  Each workgroup
+//   * streams its B block (k-rows of 256 bytes) and the matching A columns
+//     global -> LDS with LDS-DMA through a ring of NS stages of 64 k-rows;
+//   * gives each of its 4 waves 32 of the 128 columns, so waves never need
+//     to combine results; B fragments come from ds_read_b64_tr_b16 on the
+//     [k][n] tile, A fragments from ds_read_b128 (v_mfma_f32_16x16x32, the M
+//     rows in the MFMA's 16-wide dimension);
+//   * with S == 1 writes C directly; otherwise writes its fp32 partial block
+//     to the workspace, and skinny_reduce_kernel sums the S partials, adds the
+//     bias and rounds to the output type.
+#pragma once
+
+#include "device_common.h"
+
+namespace cmpext3 {
+
+constexpr int kWideStrip = 128;  // columns per workgroup
+constexpr int kWideKS = 64;      // k rows per ring stage
+
+template <int MB>
+struct WideShape {
+  static constexpr int B_BYTES = kWideKS * kWideStrip * 2;  // 16 KB, rows of 256 bytes
+  static constexpr int A_BYTES = MB * 16 * 128;             // rows of 64 k = 128 bytes
+  static constexpr int STAGE = B_BYTES + A_BYTES;
+  static constexpr int NS = (160 * 1024) / STAGE > 8 ? 8 : (160 * 1024) / STAGE;
+  static constexpr int B_DMA = B_BYTES / 4096;  // per wave
+  static constexpr int A_DMA_WG = A_BYTES / 1024;  // per workgroup, dealt round-robin to waves
+  static constexpr int A_HI = (A_DMA_WG + 3) / 4;  // A loads of waves < A_DMA_WG % 4 (or all)
+  static constexpr int A_LO = A_DMA_WG / 4;
+  static_assert(NS >= 4 && (NS - 2) * (B_DMA + A_HI) <= 63, "ring depth / vmcnt range");
+};
+
+// Byte offset in a B stage of row k, 16-column segment seg (0..7): the
+// segments are XORed with (k%4) + 4*((k/8)%2), so a transposing read (rows
+// k..k+3 and k+8..k+11 of one segment, 32 lanes) hits 8 distinct 32-byte
+// bank slots.
+__device__ __forceinline__ int wide_swz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
+__device__ __forceinline__ uint32_t wide_off(int k, int seg) {
+  return (uint32_t)(k * 256 + ((seg ^ wide_swz(k)) << 5));
+}
+
+template <typename T, int MB>
+__global__ void __launch_bounds__(256) gemm_skinny_wide_kernel(const GemmParams p, float* ws, int splits,
+                                                               int ksplit) {
+  using S = WideShape<MB>;
+  constexpr int NS = S::NS;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * S::STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int strip = blockIdx.x / splits;
+  const int split = blockIdx.x - strip * splits;
+  const int n0 = strip * kWideStrip;
+  const int M = p.M, N = p.N;
+  const int kbeg = split * ksplit;
+  const int kend = min(p.K, kbeg + ksplit);
+  const int64_t bz = blockIdx.z;
+  const int64_t lda = p.lda, ldb = p.ldb;
+  const T* Ab = (const T*)p.A + bz * p.stride_a + kbeg;
+  const T* Bb = (const T*)p.B + bz * p.stride_b + (int64_t)kbeg * ldb + n0;
+  const int klen = kend - kbeg;
+
+  // ---- DMA sources (inverse of the LDS layouts), relative to the stage's k0 ----
+  uint32_t b_off[S::B_DMA];
+  int b_k[S::B_DMA];
+#pragma unroll
+  for (int i = 0; i < S::B_DMA; ++i) {
+    const int row = 4 * (wave * S::B_DMA + i) + (lane >> 4);  // 4 rows of 256 bytes per load
+    const int seg = ((lane & 15) >> 1) ^ wide_swz(row);
+    const int col = seg * 16 + (lane & 1) * 8;
+    b_off[i] = (n0 + col < N) ? (uint32_t)(row * ldb + col) * (uint32_t)sizeof(T) : kBufOOB;
+    b_k[i] = row;
+  }
+  const int a_cnt = wave < (S::A_DMA_WG & 3) || (S::A_DMA_WG & 3) == 0 ? S::A_HI : S::A_LO;
+  uint32_t a_off[S::A_HI];
+  int a_k[S::A_HI];
+#pragma unroll
+  for (int j = 0; j < S::A_HI; ++j) {
+    int row, chunk;
+    dma128_geom(4 * j + wave, lane, row, chunk);
+    a_off[j] = (row < M) ? (uint32_t)(row * lda + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
+    a_k[j] = 8 * chunk;
+  }
+  auto load_stage = [&](int st) {
+    const int k0 = st * kWideKS;
+    const uint32_t dst = lds_addr(smem) + (uint32_t)((st % NS) * S::STAGE);
+    const int krem = klen - k0;
+    const i32x4 rb = make_rsrc_sgpr(Bb + (int64_t)k0 * ldb);
+    const i32x4 ra = make_rsrc_sgpr(Ab + k0);
+#pragma unroll
+    for (int i = 0; i < S::B_DMA; ++i)
+      dma_load16(rb, b_k[i] < krem ? b_off[i] : kBufOOB, dst + (wave * S::B_DMA + i) * 1024);
+#pragma unroll
+    for (int j = 0; j < S::A_HI; ++j)
+      if (j < a_cnt)
+        dma_load16(ra, a_k[j] < krem ? a_off[j] : kBufOOB, dst + S::B_BYTES + (4 * j + wave) * 1024);
+  };
+  // Wait until at most NS-2 younger stages' DMA are in flight, then barrier.
+  auto certify = [&]() {
+    if (a_cnt == S::A_HI)
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 2) * (S::B_DMA + S::A_HI)) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 2) * (S::B_DMA + S::A_LO)) : "memory");
+  };
+
+  // ---- fragments: lane (c = l%16, g = l/16); wave owns columns 32w .. 32w+31 ----
+  const int c = lane & 15, g = lane >> 4;
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  f32x4 acc[2][MB];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[h][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute_stage = [&](int st) {
+    const unsigned char* stage = smem + (st % NS) * S::STAGE;
+#pragma unroll
+    for (int kb = 0; kb < kWideKS; kb += 32) {
+      u32x4 af[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        af[mb] = *(const u32x4*)(stage + S::B_BYTES + lds_off128(16 * mb + c, kb / 8 + g));
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int seg = 2 * wave + h;
+        u32x4 bf;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int k = kb + 8 * g + 4 * r + (c >> 2);
+          const unsigned char* q = stage + wide_off(k, seg) + 8 * (c & 3);
+          const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q);
+          const u32x2 v2 = __builtin_bit_cast(u32x2, v);
+          bf[2 * r] = v2.x;
+          bf[2 * r + 1] = v2.y;
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[h][mb] = Mfma<T>::mma(bf, af[mb], acc[h][mb]);
+      }
+    }
+  };
+
+  const int nst = (klen + kWideKS - 1) / kWideKS;
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t) load_stage(t);
+  certify();  // stage 0
+  for (int st = 0; st < nst; ++st) {
+    load_stage(st + NS - 1);
+    compute_stage(st);
+    certify();  // stage st+1
+  }
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // no LDS DMA may outlive the workgroup
+
+  // acc[h][mb][r] = C[16*mb + c][n0 + 32*wave + 16*h + 4*g + r]
+  const uint16_t* bias = (const uint16_t*)p.bias;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = 16 * mb + c;
+    if (m >= M) continue;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int n = n0 + 32 * wave + 16 * h + 4 * g;
+      if (n >= N) continue;  // N % 8 == 0: the four columns are all in or all out
+      if (splits == 1) {
+        uint16_t* crow = (uint16_t*)((T*)p.C + bz * p.stride_c + (int64_t)m * p.ldc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = acc[h][mb][r];
+          if (bias) x += from_bits<T>(bias[n + r]);
+          crow[n + r] = to_bits<T>(x);
+        }
+      } else {
+        float* w = ws + (((int64_t)split * gridDim.z + bz) * M + m) * N + n;
+        *(f32x4*)w = acc[h][mb];
+      }
+    }
+  }
+}
+
+// C = sum over the S partial blocks in the workspace (+ bias), rounded to T.
+// One thread per four consecutive columns.
+template <typename T>
+__global__ void __launch_bounds__(256) skinny_reduce_kernel(const GemmParams p, const float* ws, int splits,
+                                                            int batch) {
+  const int M = p.M, N = p.N;
+  const int64_t quads = (int64_t)batch * M * (N / 4);
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= quads) return;
+  const int64_t per_batch = (int64_t)M * (N / 4);
+  const int64_t bz = q / per_batch;
+  const int64_t rem = q - bz * per_batch;
+  const int m = (int)(rem / (N / 4));
+  const int n = (int)(rem - (int64_t)m * (N / 4)) * 4;
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < splits; ++sp) s += *(const f32x4*)(ws + (((int64_t)sp * batch + bz) * M + m) * N + n);
+  const uint16_t* bias = (const uint16_t*)p.bias;
+  uint16_t* crow = (uint16_t*)((T*)p.C + bz * p.stride_c + (int64_t)m * p.ldc);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float x = s[r];
+    if (bias) x += from_bits<T>(bias[n + r]);
+    crow[n + r] = to_bits<T>(x);
+  }
+}
+
+}  // namespace cmpext3

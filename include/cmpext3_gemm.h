@@ -67,7 +67,11 @@ int cmpext3_matmul_fp32(const float* A, const float* B, float* C, int M, int N, 
  * with A_b = A + b*stride_a (elements), etc.; op(B) = B for CMPEXT3_B_KN and
  * B^T for CMPEXT3_B_NK.  lda/ldb/ldc are row pitches in elements; bias is
  * NULL or a length-N vector of the same dtype added to every row before the
- * final rounding.
+ * final rounding.  `workspace` (16-byte aligned device memory, or NULL) of
+ * `workspace_bytes` bytes lets the skinny-M path split K across workgroups;
+ * cmpext3_gemm_workspace_size() says how much it can use.  Its contents need
+ * no initialisation and are dead after the call's kernels have run (calls
+ * that share a workspace must be ordered on one stream).
  * Replaces the host loop of custom_bmm_forward (src/main.cpp:313-351: one
  * launch per batch entry) with one launch, and the weight.t().contiguous()
  * copy plus separate bias kernel of custom_linear_forward
@@ -78,19 +82,29 @@ int cmpext3_gemm_ex(int dtype, int b_layout,
                     const void* B, int64_t ldb, int64_t stride_b,
                     void* C, int64_t ldc, int64_t stride_c,
                     const void* bias,
-                    int M, int N, int K, int batch, void* stream);
+                    int M, int N, int K, int batch,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Bytes of workspace cmpext3_gemm_ex can use for these arguments (packed
+ * operands, 16-byte aligned); 0 when the chosen kernel needs none, or a
+ * negative CMPEXT3_ERR_*.  Host only.  No counterpart in the reference, whose
+ * kernels never split K (one launch per product, src/main.cpp:203-227).
+ */
+int64_t cmpext3_gemm_workspace_size(int dtype, int b_layout, int M, int N, int K, int batch);
 
 /*
  * Kernel selection, host only (no GPU needed): writes a one-line description
  * of the kernel cmpext3_gemm_ex would launch for these arguments into buf and
  * returns the kernel id (>= 0) or a negative CMPEXT3_ERR_*.  `align` is the
- * largest power of two (up to 16) dividing the byte address of every operand.
+ * largest power of two (up to 16) dividing the byte address of every operand;
+ * `workspace_bytes` is the workspace the call would provide.
  * No counterpart in the reference, whose tile choice is fixed at compile time
  * (fp16_matmul.cu:12-22, bf16_matmul.cu:11-21, fp32_matmul.cu:10-14).
  */
 int cmpext3_gemm_plan(int dtype, int b_layout, int M, int N, int K,
                       int64_t lda, int64_t ldb, int64_t ldc, int align, int has_bias, int batch,
-                      char* buf, int buflen);
+                      int64_t workspace_bytes, char* buf, int buflen);
 
 /* Text for a status code returned by the entry points above. */
 const char* cmpext3_status_string(int status);

@@ -21,7 +21,7 @@ def declared_symbols():
 def test_header_declares_expected_entry_points():
     syms = declared_symbols()
     for s in ["cmpext3_matmul_fp16", "cmpext3_matmul_bf16", "cmpext3_matmul_fp32", "cmpext3_gemm_ex",
-              "cmpext3_gemm_plan", "cmpext3_status_string", "cmpext3_version"]:
+              "cmpext3_gemm_workspace_size", "cmpext3_gemm_plan", "cmpext3_status_string", "cmpext3_version"]:
         assert s in syms
 
 
@@ -55,14 +55,26 @@ def test_gemm_ex_rejects_before_launch(kw, err):
     st = cabi.lib().cmpext3_gemm_ex(args["dtype"], args["layout"], args["A"], args["lda"], args["stride_a"],
                                     args["B"], args["ldb"], args["stride_b"], args["C"], args["ldc"],
                                     args["stride_c"], args["bias"], args["M"], args["N"], args["K"],
-                                    args["batch"], None)
+                                    args["batch"], None, 0, None)
     assert st == err
 
 
 def test_empty_problems_launch_nothing():
     lib = cabi.lib()
     # M == 0, N == 0 or batch == 0: success without touching the (null) pointers or the GPU
-    assert lib.cmpext3_gemm_ex(cabi.F16, cabi.B_KN, None, 8, 0, None, 8, 0, None, 8, 0, None, 0, 8, 8, 1, None) == 0
-    assert lib.cmpext3_gemm_ex(cabi.F32, cabi.B_KN, None, 8, 0, None, 8, 0, None, 8, 0, None, 8, 0, 8, 1, None) == 0
-    assert lib.cmpext3_gemm_ex(cabi.BF16, cabi.B_NK, None, 8, 0, None, 8, 0, None, 8, 0, None, 8, 8, 8, 0, None) == 0
+    assert lib.cmpext3_gemm_ex(cabi.F16, cabi.B_KN, None, 8, 0, None, 8, 0, None, 8, 0, None, 0, 8, 8, 1, None, 0,
+                               None) == 0
+    assert lib.cmpext3_gemm_ex(cabi.F32, cabi.B_KN, None, 8, 0, None, 8, 0, None, 8, 0, None, 8, 0, 8, 1, None, 0,
+                               None) == 0
+    assert lib.cmpext3_gemm_ex(cabi.BF16, cabi.B_NK, None, 8, 0, None, 8, 0, None, 8, 0, None, 8, 8, 8, 0, None, 0,
+                               None) == 0
     assert lib.cmpext3_matmul_fp16(None, None, None, 0, 0, 0, None) == 0
+
+
+def test_workspace_size_query():
+    # decode shape: 128-column strips x 4 K splits of fp32 partials
+    assert cabi.workspace_size(cabi.F16, cabi.B_KN, 16, 8192, 8192) == 4 * 16 * 8192 * 4
+    assert cabi.workspace_size(cabi.F16, cabi.B_KN, 4096, 4096, 4096) == 0   # tiled kernel: none
+    assert cabi.workspace_size(cabi.F32, cabi.B_KN, 16, 8192, 8192) == 0
+    assert cabi.workspace_size(cabi.F16, cabi.B_KN, 16, 32768, 4096) == 0    # enough strips: no split
+    assert cabi.workspace_size(7, cabi.B_KN, 16, 64, 64) == cabi.ERR_UNSUPPORTED

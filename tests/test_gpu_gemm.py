@@ -23,8 +23,8 @@ pytestmark = pytest.mark.gpu
 DT = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
 CODE = {"fp16": cabi.F16, "bf16": cabi.BF16, "fp32": cabi.F32}
 MATMUL = {"fp16": cmpext3.fp16_matmul, "bf16": cmpext3.bf16_matmul, "fp32": cmpext3.fp32_matmul}
-KERNEL_NAMES = ["tile256x256", "tile256x224", "tile128x128", "skinny", "f32tile128x128", "f32tile64x64",
-                "generic64x64"]
+KERNEL_NAMES = ["tile256x256", "tile256x224", "tile128x128", "skinny", "skinny_wide", "f32tile128x128",
+                "f32tile64x64", "generic64x64"]
 SEEN_KERNELS = set()
 
 
@@ -92,11 +92,21 @@ def test_tiled_shapes(dtype, M, N, K, kernel):
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("M,N,K", [(1, 8192, 1024), (16, 256, 8192), (17, 200, 72), (33, 96, 40),
-                                   (64, 1024, 512), (5, 2, 8)])
+                                   (64, 1024, 512), (5, 8, 8), (48, 8200, 2056)])
 def test_skinny(dtype, M, N, K):
-    assert note_kernel(dtype, M, N, K) == "skinny"
+    """Binding (wide strips + split K when a workspace helps) and C ABI without
+    workspace (narrow strips) both against the oracle."""
+    assert note_kernel(dtype, M, N, K) in ("skinny", "skinny_wide")
     a, b, out = run_matmul(dtype, M, N, K, seed=M)
     assert err_vs_oracle(out, a, b, dtype) <= O.TOLERANCE[dtype]
+    kid, desc = cabi.plan(CODE[dtype], cabi.B_KN, M, N, K)          # no workspace
+    name = desc.split()[0].split("=")[1]
+    assert name in ("skinny", "skinny_wide")                        # wide only if it needs no split
+    SEEN_KERNELS.add(name)
+    c = torch.empty(M, N, dtype=DT[dtype], device="cuda")
+    assert cabi.matmul(CODE[dtype], a.cuda(), b.cuda(), c, M, N, K) == cabi.OK
+    torch.cuda.synchronize()
+    assert err_vs_oracle(c, a, b, dtype) <= O.TOLERANCE[dtype]
 
 
 @pytest.mark.parametrize("M,N,K,kernel", [(512, 512, 512, "f32tile64x64"), (65, 47, 3, "f32tile64x64"),
@@ -210,7 +220,8 @@ def test_c_abi_matches_binding(dtype):
         assert st == cabi.OK
         torch.cuda.synchronize()
         assert torch.equal(c, c2)
-        assert torch.equal(c, MATMUL[dtype](ag, bg))
+        if cabi.workspace_size(CODE[dtype], cabi.B_KN, M, N, K) == 0:
+            assert torch.equal(c, MATMUL[dtype](ag, bg))
         assert err_vs_oracle(c, a, b, dtype) <= O.TOLERANCE[dtype]
 
 
@@ -235,10 +246,19 @@ def _full_config_check(name, via_cabi=False):
     note_kernel(dtype, M, N, K)
     out = MATMUL[dtype](ag, bg)
     if via_cabi:
+        # same kernel through the C ABI (with the workspace the binding uses): bit-identical
         c2 = torch.empty_like(out)
-        assert cabi.matmul(CODE[dtype], ag, bg, c2, M, N, K) == cabi.OK
+        ws_bytes = cabi.workspace_size(CODE[dtype], cabi.B_KN, M, N, K)
+        ws = torch.empty(max(ws_bytes, 0), dtype=torch.uint8, device="cuda") if ws_bytes > 0 else None
+        assert cabi.gemm_ex(CODE[dtype], cabi.B_KN, ag, K, 0, bg, N, 0, c2, N, 0, None, M, N, K, 1, ws) == cabi.OK
         torch.cuda.synchronize()
         assert torch.equal(out, c2)
+        # the reference-shaped entry point (no workspace) within tolerance
+        c3 = torch.empty_like(out)
+        assert cabi.matmul(CODE[dtype], ag, bg, c3, M, N, K) == cabi.OK
+        torch.cuda.synchronize()
+        e3 = ((c3.double() - out.double()).norm() / out.double().norm()).item()
+        assert e3 <= O.TOLERANCE[dtype], e3
     torch.cuda.synchronize()
     tol = O.TOLERANCE[dtype]
     out_c = out.cpu()

@@ -3,7 +3,7 @@ import pytest
 
 from cmp_ext_amd import cabi
 
-K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC = range(7)
+K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKINNY_WIDE = range(8)
 
 
 @pytest.mark.parametrize("dtype,M,N,K,expect", [
@@ -21,12 +21,24 @@ def test_config_kernel_choice(dtype, M, N, K, expect):
     assert kid == expect, desc
 
 
+def test_skinny_wide_needs_workspace():
+    need = cabi.workspace_size(cabi.F16, cabi.B_KN, 16, 8192, 8192)
+    kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 16, 8192, 8192, workspace_bytes=need)
+    assert kid == K_SKINNY_WIDE and "splits=4" in desc and "ksplit=2048" in desc and "grid=1x256x1" in desc
+    kid, _ = cabi.plan(cabi.F16, cabi.B_KN, 16, 8192, 8192, workspace_bytes=need - 1)
+    assert kid == K_SKINNY                      # too little workspace: narrow strips, no split
+    kid, desc = cabi.plan(cabi.BF16, cabi.B_KN, 16, 32768, 4096)
+    assert kid == K_SKINNY_WIDE and "splits=1" in desc   # 256 strips: no split, no workspace
+    kid, _ = cabi.plan(cabi.F16, cabi.B_KN, 17, 200, 72, workspace_bytes=1 << 30)
+    assert kid == K_SKINNY                      # tiny grid either way: narrow has more workgroups
+
+
 def test_skinny_parameters():
     kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 16, 8192, 8192)
     assert kid == K_SKINNY
-    assert "mb=1" in desc and "k_per_wave=1024" in desc and "grid=1x256x1" in desc
-    kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 33, 100, 72)
-    assert kid == K_SKINNY and "mb=3" in desc and "k_per_wave=32" in desc
+    assert "mb=1" in desc and "grid=1x256x1" in desc and "threads=256" in desc
+    kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 33, 104, 72)
+    assert kid == K_SKINNY and "mb=3" in desc and "grid=1x4x1" in desc
 
 
 @pytest.mark.parametrize("M,N,K,layout,align,expect", [
@@ -35,7 +47,8 @@ def test_skinny_parameters():
     (300, 7, 64, cabi.B_NK, 16, K_GENERIC),     # ... which N = 7 is not
     (300, 64, 33, cabi.B_KN, 16, K_GENERIC),    # K % 8 != 0
     (300, 64, 64, cabi.B_KN, 8, K_GENERIC),     # misaligned operand
-    (16, 63, 64, cabi.B_KN, 16, K_GENERIC),     # skinny needs even N
+    (16, 63, 64, cabi.B_KN, 16, K_GENERIC),     # skinny needs N % 8 == 0
+    (16, 100, 64, cabi.B_KN, 16, K_GENERIC),
     (16, 64, 60, cabi.B_KN, 16, K_GENERIC),     # skinny needs K % 8 == 0
     (16, 64, 64, cabi.B_NK, 16, K_TILE128),     # skinny is KN only
 ])
