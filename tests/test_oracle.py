@@ -209,3 +209,16 @@ def test_planted_mistakes_are_caught(golden, mutant):
     a, b = a.reshape(M, -1), b.reshape(-1, N)
     out = mutant(a, b)
     assert out.shape != exp.shape or O.rel_frobenius(out, exp) > O.TOLERANCE["fp16"]
+
+
+def test_cfg1_cpu_reference_path_within_fp32_bound():
+    """Config 1 of the benchmark contract: the reference CPU path (torch.matmul
+    on CPU) on the seeded 512^3 fp32 inputs, against the float64 oracle."""
+    c = O.CONFIGS["cfg1_fp32_512"]
+    a, b = O.make_inputs(c["dtype"], c["M"], c["N"], c["K"], c["dist"], c.get("scale", 1.0), 0)
+    out = O.cpu_matmul(a, b)
+    assert out.dtype == torch.float32 and out.shape == (512, 512)
+    err = O.reference_check(out, a, b, "fp32")
+    assert 0.0 < err <= O.TOLERANCE["fp32"]
+    # A planted mistake (operand transposed) is far outside the bound.
+    assert O.reference_check(O.cpu_matmul(a, b.T.contiguous()), a, b, "fp32") > 0.5
