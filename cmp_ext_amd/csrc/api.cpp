@@ -43,6 +43,7 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
       return launch_skinny((DType)dtype, plan.mb, p, grid, s);
     case kF32Tile128:
     case kF32Tile64:
+    case kF32Tile96x64:
       return launch_f32(plan.kernel, lay, p, grid, s);
     case kGeneric16:
       return launch_generic((DType)dtype, lay, p, grid, s);

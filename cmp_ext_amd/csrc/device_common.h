@@ -52,6 +52,14 @@ __device__ __forceinline__ void dma_load16(i32x4 rsrc, uint32_t voff, uint32_t l
                : "v"(voff), "s"(rsrc), "s"(lds_addr)
                : "memory", "m0");
 }
+// Same with 4 bytes per lane (LDS destination lds_addr + 4 * lane): any
+// 4-byte-aligned source, e.g. fp32 rows of odd length.
+__device__ __forceinline__ void dma_load4(i32x4 rsrc, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(lds_addr)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(size_t)(__attribute__((address_space(3))) const void*)p;
@@ -65,6 +73,11 @@ __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t
 }
 __device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+}
+// Vector store of 4 bytes; an offset past num_records (kBufOOB) is dropped by
+// the hardware, which is how edge elements are masked without branches.
+__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, 0);
 }
 
 // ---------------------------------------------------------------------------

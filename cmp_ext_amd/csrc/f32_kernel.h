@@ -6,46 +6,64 @@
 // accumulation) instead of the reference's separate __fmul_rn/__fadd_rn SIMT
 // loop, which exists only to dodge a GA100 FMA limit (fp32_matmul.cu:20-26).
 //
-// Any alignment is accepted: every global access is a 32-bit buffer load of
-// one element, predicated by an out-of-range offset (hardware zero-fill), so
-// ragged shapes such as 4097 x 3001 x 2049 need no special casing.  Per BK=16
-// step a thread issues BM/16 + BN/16 such loads; the matrix-core time of the
-// step (BM*BN*16*2 flop at 256 flop/clk/CU) is far longer than their issue
-// time, so narrow loads cost nothing here.
+// Any alignment is accepted: global memory is read by 4-byte LDS-DMA
+// (buffer_load_dword ... lds, 256 contiguous LDS bytes per instruction), with
+// an out-of-range offset (hardware zero-fill) for every element past M, N or
+// K, so ragged shapes such as 4097 x 3001 x 2049 need no special casing.  The
+// DMA fills a ring of NS stages of BK = 16 k; each wave counts its own DMA in
+// vmcnt, and one "s_waitcnt vmcnt; s_barrier" per step certifies that the
+// next stage is complete and that the slot about to be refilled is free, so
+// NS-2 stages of loads are always in flight without staging registers.
 //
-// LDS holds A as [m][k] and B as [n][k] (transposed on store for the KN
-// layout), rows of 16 floats padded to 20 (80 bytes: 16-byte aligned, and 16
-// consecutive rows start in 16 distinct 16-byte bank groups).  MFMA k-step s
-// of lane group g uses k = 4g + s, so one ds_read_b128 per fragment feeds four
-// MFMAs.
+// LDS layouts (per stage):
+//   A, and B given as [N,K]: [row][k], rows of 16 floats (64 bytes), 16-byte
+//     chunk c of row r stored at chunk c ^ ((r/4)%4) (f32_off): a fragment
+//     read (16 consecutive rows at one chunk, ds_read_b128) is conflict free,
+//     and one DMA instruction writes 4 whole rows.
+//   B given as [K,N]: [k][n], rows of BN floats, 16-float segment s of row k
+//     stored at segment s ^ ((k/4)%4): the fragment read of MFMA step s
+//     (rows s, 4+s, 8+s, 12+s at 16 columns, ds_read_b32) hits 64 distinct
+//     banks, and one DMA instruction writes 64 consecutive floats of a row.
+// MFMA k-step s of lane group g uses k = 4g + s, so one ds_read_b128 per A
+// fragment feeds four MFMAs.
 #pragma once
 
 #include "device_common.h"
 
 namespace cmpext3 {
 
-template <int BM, int BN>
+template <int BM, int BN, int NS_>
 struct F32Shape {
   static constexpr int BK = 16;
-  static constexpr int LDR = 20;  // floats per LDS row
+  static constexpr int NS = NS_;
   static constexpr int NT = 256;  // 2 x 2 waves
   static constexpr int WTM = BM / 2, WTN = BN / 2;
   static constexpr int FM = WTM / 16, FN = WTN / 16;
-  static constexpr int A_LD = BM * BK / NT;
-  static constexpr int B_LD = BN * BK / NT;
-  static constexpr int STAGE = (BM + BN) * LDR;  // floats
-  static_assert(BM * BK % NT == 0 && BN * BK % NT == 0, "tile");
+  static constexpr int A_BYTES = BM * BK * 4;
+  static constexpr int B_BYTES = BN * BK * 4;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int A_DMA = A_BYTES / 256 / 4;  // 256-byte DMA instructions per wave per stage
+  static constexpr int B_DMA = B_BYTES / 256 / 4;
+  static constexpr int DMA = A_DMA + B_DMA;
+  static_assert(BN % 64 == 0 && BM % 32 == 0, "whole DMA instructions per wave, 64-float B rows");
+  static_assert(NS >= 2 && (NS - 2) * DMA <= 63, "ring depth / vmcnt range");
+  static_assert(NS * STAGE <= 160 * 1024, "LDS");
 };
 
-template <bool KN, int BM, int BN>
+// Byte offset of 16-byte chunk `chunk` (0..3) of row `row` in a [row][16 floats] block.
+__device__ __forceinline__ uint32_t f32_off(int row, int chunk) {
+  return (uint32_t)((row >> 2) * 256 + 16 * (4 * (row & 3) + (chunk ^ ((row >> 2) & 3))));
+}
+
+template <bool KN, int BM, int BN, int NS>
 __global__ void __launch_bounds__(256) gemm_f32_kernel(const GemmParams p) {
-  using S = F32Shape<BM, BN>;
+  using S = F32Shape<BM, BN, NS>;
   constexpr int FM = S::FM, FN = S::FN;
-  __shared__ __attribute__((aligned(16))) float smem[2 * S::STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * S::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
   int tm, tn;
@@ -58,64 +76,62 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(const GemmParams p) {
   const float* Bbase = KN ? (const float*)p.B + bz * p.stride_b + n0
                           : (const float*)p.B + bz * p.stride_b + (int64_t)n0 * ldb;
 
-  // A element e = tid + i*256: row e/16, k e%16 (16 consecutive k per row).
-  uint32_t a_goff[S::A_LD], a_soff[S::A_LD];
-  int a_k[S::A_LD];
-  bool a_ok[S::A_LD];
+  // ---- DMA sources: the inverse of the LDS layouts, relative to the stage's k0 ----
+  // [row][k] blocks: instruction t writes rows 4t..4t+3; lane l lands in row
+  // 4t + l/16 at chunk slot (l/4)%4, element l%4, which holds data chunk
+  // slot ^ (t%4).
+  uint32_t a_off[S::A_DMA];
+  int a_k[S::A_DMA];
 #pragma unroll
-  for (int i = 0; i < S::A_LD; ++i) {
-    const int e = tid + i * S::NT;
-    const int row = e >> 4, kk = e & 15;
-    a_ok[i] = m0 + row < M;
-    a_goff[i] = (uint32_t)(row * lda + kk) * 4u;
-    a_soff[i] = (uint32_t)(row * S::LDR + kk);
-    a_k[i] = kk;
+  for (int i = 0; i < S::A_DMA; ++i) {
+    const int t = wave * S::A_DMA + i;
+    const int row = 4 * t + (lane >> 4);
+    const int k = 4 * (((lane >> 2) & 3) ^ (t & 3)) + (lane & 3);
+    a_off[i] = (m0 + row < M) ? (uint32_t)(row * lda + k) * 4u : kBufOOB;
+    a_k[i] = k;
   }
-  // B: KN element e: k e/BN, n e%BN (coalesced along n); NK like A.
-  uint32_t b_goff[S::B_LD], b_soff[S::B_LD];
-  int b_k[S::B_LD];
-  bool b_ok[S::B_LD];
+  // B: [K,N] -> instruction t writes row k = t / (BN/64), floats 64*(t%(BN/64)) ..
+  //    +63; lane l lands in segment slot 4*(t%(BN/64)) + l/16, which holds data
+  //    segment slot ^ ((k/4)%4).  [N,K] -> as A.
+  uint32_t b_off[S::B_DMA];
+  int b_k[S::B_DMA];
 #pragma unroll
-  for (int i = 0; i < S::B_LD; ++i) {
-    const int e = tid + i * S::NT;
-    int n, kk;
+  for (int i = 0; i < S::B_DMA; ++i) {
+    const int t = wave * S::B_DMA + i;
     if (KN) {
-      kk = e / BN;
-      n = e % BN;
-      b_goff[i] = (uint32_t)(kk * ldb + n) * 4u;
+      constexpr int PER_ROW = BN / 64;
+      const int k = t / PER_ROW;
+      const int seg = (4 * (t % PER_ROW) + (lane >> 4)) ^ ((k >> 2) & 3);
+      const int n = 16 * seg + (lane & 15);
+      b_off[i] = (n0 + n < N) ? (uint32_t)(k * ldb + n) * 4u : kBufOOB;
+      b_k[i] = k;
     } else {
-      n = e >> 4;
-      kk = e & 15;
-      b_goff[i] = (uint32_t)(n * ldb + kk) * 4u;
+      const int row = 4 * t + (lane >> 4);
+      const int k = 4 * (((lane >> 2) & 3) ^ (t & 3)) + (lane & 3);
+      b_off[i] = (n0 + row < N) ? (uint32_t)(row * ldb + k) * 4u : kBufOOB;
+      b_k[i] = k;
     }
-    b_ok[i] = n0 + n < N;
-    b_soff[i] = (uint32_t)(n * S::LDR + kk);
-    b_k[i] = kk;
   }
-
-  float ra[S::A_LD], rb[S::B_LD];
-  auto load_tile = [&](int k0) {
-    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(Abase + k0);
-    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(KN ? Bbase + (int64_t)k0 * ldb : Bbase + k0);
+  auto load_stage = [&](int st) {
+    const int k0 = st * S::BK;
+    const int krem = K - k0;
+    const uint32_t dst = lds_addr(smem) + (uint32_t)((st % NS) * S::STAGE);
+    const i32x4 ra = make_rsrc_sgpr(Abase + k0);
+    const i32x4 rb = make_rsrc_sgpr(KN ? Bbase + (int64_t)k0 * ldb : Bbase + k0);
 #pragma unroll
-    for (int i = 0; i < S::A_LD; ++i)
-      ra[i] = __uint_as_float(buf_load4(a_rsrc, (a_ok[i] && k0 + a_k[i] < K) ? a_goff[i] : kBufOOB));
+    for (int i = 0; i < S::A_DMA; ++i)
+      dma_load4(ra, a_k[i] < krem ? a_off[i] : kBufOOB, dst + (wave * S::A_DMA + i) * 256);
 #pragma unroll
-    for (int i = 0; i < S::B_LD; ++i)
-      rb[i] = __uint_as_float(buf_load4(b_rsrc, (b_ok[i] && k0 + b_k[i] < K) ? b_goff[i] : kBufOOB));
-  };
-  auto store_tile = [&](int stage) {
-    float* sA = smem + stage * S::STAGE;
-    float* sB = sA + BM * S::LDR;
-#pragma unroll
-    for (int i = 0; i < S::A_LD; ++i) sA[a_soff[i]] = ra[i];
-#pragma unroll
-    for (int i = 0; i < S::B_LD; ++i) sB[b_soff[i]] = rb[i];
+    for (int i = 0; i < S::B_DMA; ++i)
+      dma_load4(rb, b_k[i] < krem ? b_off[i] : kBufOOB, dst + S::A_BYTES + (wave * S::B_DMA + i) * 256);
   };
 
+  // ---- fragments: lane (r16 = l%16, g = l/16) ----
   const int r16 = lane & 15, g = lane >> 4;
-  const int fa = (wm * S::WTM + r16) * S::LDR + 4 * g;
-  const int fb = (wn * S::WTN + r16) * S::LDR + 4 * g;
+  const uint32_t fa = f32_off(wm * S::WTM + r16, g);  // + 1024 per 16 rows
+  const uint32_t fb_nk = S::A_BYTES + f32_off(wn * S::WTN + r16, g);
+  // [K,N] B, MFMA step s, fragment j: row 4g + s, segment (wn*FN + j) ^ g, column r16.
+  const uint32_t fb_kn = S::A_BYTES + (uint32_t)(4 * g * BN * 4 + 4 * r16);
 
   f32x4 acc[FM][FN];
 #pragma unroll
@@ -123,54 +139,75 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(const GemmParams p) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int stage) {
-    const float* sA = smem + stage * S::STAGE;
-    const float* sB = sA + BM * S::LDR;
-    f32x4 af[FM], bf[FN];
+  auto compute_stage = [&](int st) {
+    const unsigned char* stage = smem + (st % NS) * S::STAGE;
+    f32x4 af[FM];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) af[i] = *(const f32x4*)(sA + fa + i * 16 * S::LDR);
+    for (int i = 0; i < FM; ++i) af[i] = *(const f32x4*)(stage + fa + i * 1024);
+    if (KN) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) bf[j] = *(const f32x4*)(sB + fb + j * 16 * S::LDR);
+      for (int s = 0; s < 4; ++s) {
+        float bf[FN];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+        for (int j = 0; j < FN; ++j)
+          bf[j] = *(const float*)(stage + fb_kn + s * BN * 4 + (((wn * FN + j) ^ g) << 6));
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mma_f32(bf[j][s], af[i][s], acc[i][j]);
+          for (int j = 0; j < FN; ++j) acc[i][j] = mma_f32(bf[j], af[i][s], acc[i][j]);
+      }
+    } else {
+      f32x4 bf[FN];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[j] = *(const f32x4*)(stage + fb_nk + j * 1024);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) acc[i][j] = mma_f32(bf[j][s], af[i][s], acc[i][j]);
+    }
+  };
+  auto certify = [&]() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 2) * S::DMA) : "memory");
   };
 
-  const int nk = (K + S::BK - 1) / S::BK;
-  if (nk > 0) {
-    load_tile(0);
-    store_tile(0);
+  const int nst = (K + S::BK - 1) / S::BK;
+  // Step st: DMA stage st+NS-1 (zeros past K), compute st, certify st+1.
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t) load_stage(t);
+  certify();
+  for (int st = 0; st < nst; ++st) {
+    load_stage(st + NS - 1);
+    compute_stage(st);
+    certify();
   }
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int stage = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) load_tile((kt + 1) * S::BK);
-    compute(stage);
-    if (more) store_tile(stage ^ 1);
-    __syncthreads();
-  }
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // no LDS DMA may outlive the workgroup
 
-  float* Cb = (float*)p.C + bz * p.stride_c;
+  // acc[i][j][e] = C[m0 + wm*WTM + 16i + r16][n0 + wn*WTN + 16j + 4g + e]; elements
+  // outside C get an out-of-range offset and are dropped by the store.
+  const __amdgpu_buffer_rsrc_t crs = make_rsrc((float*)p.C + bz * p.stride_c + (int64_t)m0 * p.ldc + n0);
   const float* bias = (const float*)p.bias;
+  float bv[FN][4];
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int n = n0 + wn * S::WTN + j * 16 + 4 * g + e;
+      bv[j][e] = (bias != nullptr && n < N) ? bias[n] : 0.f;
+    }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
-    const int m = m0 + wm * S::WTM + i * 16 + r16;
-    if (m >= M) continue;
-    float* crow = Cb + (int64_t)m * p.ldc;
+    const int row = wm * S::WTM + i * 16 + r16;
+    const bool row_ok = m0 + row < M;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const int n = n0 + wn * S::WTN + j * 16 + 4 * g;
+      const int col = wn * S::WTN + j * 16 + 4 * g;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        if (n + e < N) {
-          float x = acc[i][j][e];
-          if (bias) x += bias[n + e];
-          crow[n + e] = x;
-        }
+        const bool ok = row_ok && n0 + col + e < N;
+        const float x = bias != nullptr ? acc[i][j][e] + bv[j][e] : acc[i][j][e];
+        buf_store4(crs, ok ? (uint32_t)(row * p.ldc + col + e) * 4u : kBufOOB, x);
       }
     }
   }

@@ -24,7 +24,7 @@ DT = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
 CODE = {"fp16": cabi.F16, "bf16": cabi.BF16, "fp32": cabi.F32}
 MATMUL = {"fp16": cmpext3.fp16_matmul, "bf16": cmpext3.bf16_matmul, "fp32": cmpext3.fp32_matmul}
 KERNEL_NAMES = ["tile256x256", "tile256x224", "tile128x128", "skinny", "skinny_wide", "f32tile128x128",
-                "f32tile64x64", "generic64x64"]
+                "f32tile64x64", "f32tile96x64", "generic64x64"]
 SEEN_KERNELS = set()
 
 
@@ -111,7 +111,8 @@ def test_skinny(dtype, M, N, K):
 
 @pytest.mark.parametrize("M,N,K,kernel", [(512, 512, 512, "f32tile64x64"), (65, 47, 3, "f32tile64x64"),
                                           (1, 1, 1, "f32tile64x64"), (6144, 8192, 64, "f32tile128x128"),
-                                          (257, 131, 129, "f32tile64x64")])
+                                          (257, 131, 129, "f32tile64x64"),
+                                          (1440, 768, 200, "f32tile96x64"), (1439, 767, 201, "f32tile96x64")])
 def test_fp32(M, N, K, kernel):
     assert note_kernel("fp32", M, N, K) == kernel
     a, b, out = run_matmul("fp32", M, N, K, seed=3, dist="uniform")

@@ -3,7 +3,7 @@ import pytest
 
 from cmp_ext_amd import cabi
 
-K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKINNY_WIDE = range(8)
+K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKINNY_WIDE, K_F32_96 = range(9)
 
 
 @pytest.mark.parametrize("dtype,M,N,K,expect", [
@@ -11,7 +11,9 @@ K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKI
     (cabi.F16, 4096, 4096, 4096, K_TILE256),      # cfg2: 256 tiles = one per CU
     (cabi.BF16, 4096, 14336, 4096, K_TILE224),    # cfg3: 1024 tiles = 4 full waves
     (cabi.F16, 16, 8192, 8192, K_SKINNY),         # cfg4
-    (cabi.F32, 4097, 3001, 2049, K_F32_64),       # cfg5: ragged
+    (cabi.F32, 4097, 3001, 2049, K_F32_96),       # cfg5: 2021 tiles of 96x64 (<= 8 per CU)
+    (cabi.F32, 4096, 4096, 4096, K_F32_128),
+    (cabi.F32, 1440, 768, 200, K_F32_96),
     (cabi.F16, 1024, 1024, 1024, K_TILE128),      # small: more tiles wanted
     (cabi.BF16, 64, 4096, 4096, K_SKINNY),
     (cabi.BF16, 65, 4096, 4096, K_TILE128),
@@ -59,7 +61,7 @@ def test_alignment_fallbacks(M, N, K, layout, align, expect):
 
 def test_fp32_any_alignment():
     kid, _ = cabi.plan(cabi.F32, cabi.B_KN, 4097, 3001, 2049, align=4)
-    assert kid in (K_F32_64, K_F32_128)
+    assert kid in (K_F32_64, K_F32_96, K_F32_128)
 
 
 @pytest.mark.parametrize("args,err", [
