@@ -8,10 +8,10 @@ template <bool KN>
 hipError_t launch(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s) {
   switch (id) {
     case kTile256x256:
-      hipLaunchKernelGGL((gemm_tile_kernel<_Float16, KN, 256, 256, 2, 2, 5>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((gemm_tile_kernel<_Float16, KN, 256, 256, 2, 2, 2, 64>), grid, dim3(256), 0, s, p);
       break;
     case kTile256x224:
-      hipLaunchKernelGGL((gemm_tile_kernel<_Float16, KN, 256, 224, 4, 1, 5>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((gemm_tile_kernel<_Float16, KN, 256, 224, 4, 1, 2, 64>), grid, dim3(256), 0, s, p);
       break;
     case kTile128x128:
       hipLaunchKernelGGL((gemm_tile_kernel<_Float16, KN, 128, 128, 2, 2, 5>), grid, dim3(256), 0, s, p);

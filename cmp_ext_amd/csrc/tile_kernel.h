@@ -29,27 +29,30 @@
 //     the buffer descriptor's range: the hardware writes zeros into LDS and
 //     touches no memory.
 //   * Each wave owns a (BM/WM) x (BN/WN) block of 32x32 fp32 accumulators
-//     (AGPRs) fed by v_mfma_f32_32x32x16_{f16,bf16};
-//     __builtin_amdgcn_sched_group_barrier interleaves the DMA issue and the
-//     LDS reads with the MFMAs.
+//     (AGPRs) fed by v_mfma_f32_32x32x16_{f16,bf16}.  The LDS reads of the
+//     next sub-step's fragments and the DMA pieces of step t+NS-1 are spread
+//     evenly between the MFMAs of both sub-steps (16 k each), so neither the
+//     LDS queue nor the per-CU memory address FIFOs fill and hold up the
+//     matrix-core issue.
 #pragma once
 
 #include "device_common.h"
 
 namespace cmpext3 {
 
-template <int BM, int BN, int WM, int WN, bool KN, int NS_>
+template <int BM, int BN, int WM, int WN, bool KN, int NS_, int BK_>
 struct TileShape {
-  static constexpr int BK = 32;
+  static constexpr int BK = BK_;
   static constexpr int NS = NS_;
+  static constexpr int ROW = BK * 2;  // bytes per LDS row of a K-contiguous operand
   static constexpr int NT = WM * WN * 64;
   static constexpr int WTM = BM / WM;
   static constexpr int WTN = BN / WN;
   static constexpr int FM = WTM / 32;  // 32x32 accumulator blocks per wave
   static constexpr int FN = WTN / 32;
-  static constexpr int A_BYTES = BM * 64;
-  static constexpr int B_PITCH = KN ? (BN * 2 + 255) / 256 * 256 : 64;  // bytes per LDS row of B
-  static constexpr int B_BYTES = KN ? BK * B_PITCH : (BN + 63) / 64 * 64 * 64;  // rows >= BN are OOB
+  static constexpr int A_BYTES = BM * ROW;
+  static constexpr int B_PITCH = KN ? (BN * 2 + 255) / 256 * 256 : ROW;  // bytes per LDS row of B
+  static constexpr int B_BYTES = KN ? BK * B_PITCH : (BN + 63) / 64 * 64 * ROW;  // rows >= BN are OOB
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int LDS = NS * STAGE;
   static constexpr int A_DMA = A_BYTES / 1024 / 4;  // 1 KB LDS-DMA loads per wave per stage
@@ -58,12 +61,10 @@ struct TileShape {
   static_assert(NT == 256, "four waves");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
   static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "whole DMA loads per wave");
-  static_assert(NS >= 3, "ring of at least three stages");
+  static_assert(BK == 32 || BK == 64, "64- or 128-byte rows");
+  static_assert(BK == 32 ? NS >= 3 : NS == 2, "BK 32: ring of >= 3 stages; BK 64: two stages");
   static_assert(LDS <= 160 * 1024, "LDS budget");
 };
-
-// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
-constexpr int kSgMfma = 0x008, kSgDsRead = 0x100;
 
 // LDS byte offset of 16-byte chunk `chunk` (0..3) of row `row` in a tile of
 // 64-byte rows: groups of four rows fill one 256-byte bank line, chunks are
@@ -81,6 +82,21 @@ __device__ __forceinline__ void dma64_geom(int slot, int lane, int& row, int& ch
   chunk = (lane & 3) ^ (lane >> 4);
 }
 
+// K-contiguous tiles: 64-byte rows (BK = 32) use lds_off64, 128-byte rows
+// (BK = 64) use lds_off128; both are conflict free for 16 consecutive rows
+// at one chunk, and chunk 2*ks + h of either is chunk h XOR 32*ks in bytes.
+template <int BK>
+__device__ __forceinline__ uint32_t kc_off(int row, int chunk) {
+  return BK == 32 ? lds_off64(row, chunk) : lds_off128(row, chunk);
+}
+template <int BK>
+__device__ __forceinline__ void kc_geom(int slot, int lane, int& row, int& chunk) {
+  if (BK == 32)
+    dma64_geom(slot, lane, row, chunk);
+  else
+    dma128_geom(slot, lane, row, chunk);
+}
+
 // [k][n] layout of an N-contiguous B tile: rows of `pitch` bytes (a multiple
 // of 256), 64-byte segments XORed with k%4.  Lane `lane` of DMA load `slot`
 // fetches row k, columns n..n+7.
@@ -92,9 +108,9 @@ __device__ __forceinline__ void dma_kn_geom(int slot, int lane, int pitch, int& 
   n = (seg * 64 + (within & 63)) >> 1;
 }
 
-template <typename T, bool KN, int BM, int BN, int WM, int WN, int NS>
+template <typename T, bool KN, int BM, int BN, int WM, int WN, int NS, int BK = 32>
 __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmParams p) {
-  using S = TileShape<BM, BN, WM, WN, KN, NS>;
+  using S = TileShape<BM, BN, WM, WN, KN, NS, BK>;
   constexpr int FM = S::FM, FN = S::FN;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[S::LDS];
 
@@ -122,7 +138,7 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmPa
 #pragma unroll
   for (int i = 0; i < S::A_DMA; ++i) {
     int row, chunk;
-    dma64_geom(wave * S::A_DMA + i, lane, row, chunk);
+    kc_geom<BK>(wave * S::A_DMA + i, lane, row, chunk);
     a_off[i] = (m0 + row < M) ? (uint32_t)(row * lda + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
     a_kx[i] = 8 * chunk;
   }
@@ -138,7 +154,7 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmPa
       b_kx[i] = k;
     } else {
       int row, chunk;
-      dma64_geom(wave * S::B_DMA + i, lane, row, chunk);
+      kc_geom<BK>(wave * S::B_DMA + i, lane, row, chunk);
       b_off[i] = (row < BN && n0 + row < N) ? (uint32_t)(row * ldb + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
       b_kx[i] = 8 * chunk;
     }
@@ -169,12 +185,12 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmPa
   // the one two ahead has landed in this wave's share of LDS), then barrier:
   // after it, that step is complete for the whole workgroup.
   auto certify = [&]() {
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 3) * S::DMA) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(NS >= 3 ? (NS - 3) * S::DMA : 0) : "memory");
   };
 
   // ---- fragment read addresses ----
   const int r32 = lane & 31, h = lane >> 5;
-  const uint32_t fa0 = lds_off64(wm * S::WTM + r32, h);  // sub-step ks: ^ (ks << 5)
+  const uint32_t fa0 = kc_off<BK>(wm * S::WTM + r32, h);  // sub-step ks: ^ (ks << 5)
   uint32_t fb0[KN ? FN : 1];
   if (KN) {
     // transposing reads: lane (group G = lane/16, s = lane%16) points at row
@@ -187,7 +203,7 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmPa
     for (int j = 0; j < FN; ++j)
       fb0[j] = (uint32_t)(k * S::B_PITCH + (((seg0 + j) ^ (k & 3)) << 6) + 32 * (G & 1) + 8 * (s & 3));
   } else {
-    fb0[0] = lds_off64(wn * S::WTN + r32, h);
+    fb0[0] = kc_off<BK>(wn * S::WTN + r32, h);
   }
 
   f32x16 acc[FM][FN];
@@ -200,72 +216,98 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmPa
 
   typedef short s16x4 __attribute__((ext_vector_type(4)));
   u32x4 fa[2][FM], fb[2][FN];
-  auto read_frags = [&](int kt, int ks, int buf) {
+  // LDS read r (0 .. RD-1) of sub-step ks of step kt into fragment buffer buf:
+  // r < FM reads A block r; then B (two transposing reads per block for
+  // [K,N], one ds_read_b128 for [N,K]).
+  constexpr int RD = FM + (KN ? 2 : 1) * FN;
+  auto read_one = [&](int kt, int ks, int buf, int r) {
     const unsigned char* sA = smem + (kt % NS) * S::STAGE;
     const unsigned char* sB = sA + S::A_BYTES;
-    const uint32_t xa = fa0 ^ (uint32_t)(ks << 5);
-#pragma unroll
-    for (int i = 0; i < FM; ++i) fa[buf][i] = *(const u32x4*)(sA + xa + i * 2048);
-    if (KN) {
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const unsigned char* q = sB + fb0[j] + ks * 16 * S::B_PITCH;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(q));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(q + 4 * S::B_PITCH));
-        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-        fb[buf][j] = u32x4{l2.x, l2.y, h2.x, h2.y};
+    if (r < FM) {
+      fa[buf][r] = *(const u32x4*)(sA + (fa0 ^ (uint32_t)(ks << 5)) + r * 32 * S::ROW);
+    } else if (KN) {
+      const int j = (r - FM) >> 1, half = (r - FM) & 1;
+      const unsigned char* q = sB + fb0[j] + ks * 16 * S::B_PITCH + half * 4 * S::B_PITCH;
+      const u32x2 v = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q));
+      if (half == 0) {
+        fb[buf][j].x = v.x;
+        fb[buf][j].y = v.y;
+      } else {
+        fb[buf][j].z = v.x;
+        fb[buf][j].w = v.y;
       }
     } else {
-      const uint32_t xb = fb0[0] ^ (uint32_t)(ks << 5);
-#pragma unroll
-      for (int j = 0; j < FN; ++j) fb[buf][j] = *(const u32x4*)(sB + xb + j * 2048);
+      const int j = r - FM;
+      fb[buf][j] = *(const u32x4*)(sB + (fb0[0] ^ (uint32_t)(ks << 5)) + j * 32 * S::ROW);
     }
   };
-  auto mfma_one = [&](int buf, int x) {
-    const int i = x / FN, j = x % FN;
-    acc[i][j] = Mfma32<T>::mma(fb[buf][j], fa[buf][i], acc[i][j]);
-  };
-  auto mfmas = [&](int buf) {
+  // One sub-step (16 k) of MFMAs on fragment buffer `buf`, with the reads of
+  // the next sub-step's fragments (into the other buffer) spread over its
+  // first three quarters and DMA pieces [d0, d1) of step `dkt` spread evenly:
+  // short bursts keep the per-CU address FIFOs and the LDS queue from
+  // filling, which would stall the MFMA issue behind them.  A scheduling
+  // barrier after every MFMA slot keeps the compiler from regrouping them.
+  constexpr int X = FM * FN;
+  constexpr int XR = (3 * X + 3) / 4;  // MFMA slots that carry reads
+  auto substep = [&](int buf, int rkt, int rks, int d0, int d1, int dkt) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int x = 0; x < X; ++x) {
+      const int i = x / FN, j = x % FN;
+      acc[i][j] = Mfma32<T>::mma(fb[buf][j], fa[buf][i], acc[i][j]);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = Mfma32<T>::mma(fb[buf][j], fa[buf][i], acc[i][j]);
+      for (int r = 0; r < RD; ++r)
+        if (x < XR && r * XR / RD == x) read_one(rkt, rks, buf ^ 1, r);
+#pragma unroll
+      for (int d = 0; d < S::DMA; ++d)
+        if (d >= d0 && d < d1 && (d - d0) * X / (d1 - d0) == x) dma_piece(dkt, d);
+      __builtin_amdgcn_sched_barrier(0);  // keep the slots in this order
+    }
   };
-  constexpr int RD = FM + (KN ? 2 : 1) * FN;  // LDS read instructions per sub-step
 
   const int nk = (K + S::BK - 1) / S::BK;
-  if (nk > 0) {
-    // prologue: steps 0 .. NS-2 in flight; steps 0 and 1 certified
+  if constexpr (NS >= 3) {
+    if (nk > 0) {
+    // BK = 32, ring of NS stages: step t+2 is certified at the barrier that
+    // ends step t, so both sub-steps read ahead and no barrier waits on LDS.
 #pragma unroll
     for (int t = 0; t < NS - 1; ++t) load_step(t);
     certify();
-    read_frags(0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < RD; ++r) read_one(0, 0, 0, r);
     for (int kt = 0; kt < nk; ++kt) {
-      // sub-step 0 (fragments in buffer 0): read sub-step 1's fragments into
-      // buffer 1 up front, then issue step kt+NS-1's DMA pieces one per MFMA
-      // (each inline-asm DMA is a scheduling boundary, so source order holds)
-      read_frags(kt, 1, 1);
-#pragma unroll
-      for (int x = 0; x < FM * FN; ++x) {
-        mfma_one(0, x);
-        if (x < S::DMA) dma_piece(kt + NS - 1, x);
-      }
-      // sub-step 1 (buffer 1): step kt+1's first fragments into buffer 0
-      // (certified at the last barrier; after the last step this reads a
-      // stale slot, which is never used)
-      read_frags(kt + 1, 0, 0);
-      mfmas(1);
-#pragma unroll
-      for (int x = 0; x < FM * FN; ++x) {
-        __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-        if (2 * x + 2 <= RD)
-          __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
-        else if (2 * x < RD)
-          __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+      // sub-step 0 reads sub-step 1's fragments; sub-step 1 reads step kt+1's
+      // first fragments (certified at the last barrier; after the last step
+      // this reads a stale slot, which is never used).  Step kt+NS-1's DMA is
+      // split over both.
+      substep(0, kt, 1, 0, S::DMA / 2, kt + NS - 1);
+      substep(1, kt + 1, 0, S::DMA / 2, S::DMA, kt + NS - 1);
       certify();  // step kt+2
+    }
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // no LDS DMA may outlive the workgroup
+    }
+  } else if (nk > 0) {
+    // BK = 64, two stages of 64 KB (256 x 256): the barrier of step t sits
+    // before its last sub-step, once every fragment of step t is in
+    // registers and step t+1 has landed.  Right after it the freed slot
+    // starts receiving step t+2 (first half of its DMA in the last sub-step,
+    // second half in sub-step 0 of step t+1), and the last sub-step's MFMAs
+    // cover the reads of step t+1's first fragments.
+    constexpr int KS = S::BK / 16;  // sub-steps per step
+    constexpr int H = S::DMA / 2;
+    load_step(0);
+#pragma unroll
+    for (int d = 0; d < H; ++d) dma_piece(1, d);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(H) : "memory");  // step 0 landed
+#pragma unroll
+    for (int r = 0; r < RD; ++r) read_one(0, 0, 0, r);
+    for (int kt = 0; kt < nk; ++kt) {
+      substep(0, kt, 1, H, S::DMA, kt + 1);
+#pragma unroll
+      for (int ks = 1; ks < KS - 1; ++ks) substep(ks & 1, kt, ks + 1, 0, 0, 0);
+      // every fragment of step kt read, step kt+1 landed (this wave), then barrier
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" : : : "memory");
+      substep((KS - 1) & 1, kt + 1, 0, 0, H, kt + 2);
     }
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // no LDS DMA may outlive the workgroup
   }
