@@ -10,25 +10,36 @@ GEMM entry points, src/main.cpp:1594-1602, plus the dtype-specific matmuls):
 
 Every call runs the hand-written gfx950 kernels of lib/libcmpext3_gemm.so on
 PyTorch's current stream.  There is no fallback: if the compiled extension is
-missing, importing this package raises ImportError.
+missing, every operator access (and `import cmpext3`) raises ImportError; only
+the `build` submodule stays usable.
 """
 import torch  # noqa: F401  (loads PyTorch's HIP runtime before the extension binds to it)
 
+__all__ = ["fp16_matmul", "bf16_matmul", "fp32_matmul", "linear", "bmm", "plan", "version"]
+
 try:
     from . import _cmpext3 as _ext
-except ImportError as e:  # pragma: no cover - exercised only on a tree that was not built
-    raise ImportError(
-        "cmp_ext_amd: the compiled extension is missing; run `python -m cmp_ext_amd.build` "
-        f"(or __graft_entry__.build()) first ({e})"
-    ) from e
+except ImportError as _e:  # a tree that was not built: every operator access raises
+    _ext = None
+    _ext_error = _e
 
-fp16_matmul = _ext.fp16_matmul
-bf16_matmul = _ext.bf16_matmul
-fp32_matmul = _ext.fp32_matmul
-linear = _ext.linear
-bmm = _ext.bmm
-plan = _ext.plan
-version = _ext.version
-extension_path = _ext.__file__
+if _ext is not None:
+    fp16_matmul = _ext.fp16_matmul
+    bf16_matmul = _ext.bf16_matmul
+    fp32_matmul = _ext.fp32_matmul
+    linear = _ext.linear
+    bmm = _ext.bmm
+    plan = _ext.plan
+    version = _ext.version
+    extension_path = _ext.__file__
+else:
 
-__all__ = ["fp16_matmul", "bf16_matmul", "fp32_matmul", "linear", "bmm", "plan", "version"]
+    def __getattr__(name):
+        # The submodule `cmp_ext_amd.build` stays importable so that an unbuilt tree can be
+        # built; any operator (and `from cmp_ext_amd import *`, hence `import cmpext3`) fails.
+        if name not in __all__ and name != "extension_path":
+            raise AttributeError(name)
+        raise ImportError(
+            "cmp_ext_amd: the compiled extension is missing; run `python -m cmp_ext_amd.build` "
+            f"(or __graft_entry__.build()) first ({_ext_error})"
+        ) from _ext_error
