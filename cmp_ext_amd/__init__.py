@@ -6,6 +6,8 @@ GEMM entry points, src/main.cpp:1594-1602, plus the dtype-specific matmuls):
     fp16_matmul(a, b), bf16_matmul(a, b), fp32_matmul(a, b)   C = A @ B
     linear(input, weight, bias=None)                          input @ weight.T + bias
     bmm(input, mat2)                                           batched A @ B
+    conv2d(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1)
+                                                               1x1 NCHW convolution as a GEMM
     plan(dtype, M, N, K, layout="KN", batch=1, has_bias=False) kernel the selector picks
 
 Every call runs the hand-written gfx950 kernels of lib/libcmpext3_gemm.so on
@@ -15,10 +17,14 @@ the `build` submodule stays usable.
 """
 import torch  # noqa: F401  (loads PyTorch's HIP runtime before the extension binds to it)
 
-__all__ = ["fp16_matmul", "bf16_matmul", "fp32_matmul", "linear", "bmm", "plan", "version"]
+__all__ = ["fp16_matmul", "bf16_matmul", "fp32_matmul", "linear", "bmm", "conv2d", "plan", "version"]
 
 try:
     from . import _cmpext3 as _ext
+
+    _missing = [n for n in __all__ if not hasattr(_ext, n)]
+    if _missing:  # built from older sources
+        raise ImportError(f"{_ext.__file__} is stale (lacks {', '.join(_missing)}); rebuild it")
 except ImportError as _e:  # a tree that was not built: every operator access raises
     _ext = None
     _ext_error = _e
@@ -29,6 +35,7 @@ if _ext is not None:
     fp32_matmul = _ext.fp32_matmul
     linear = _ext.linear
     bmm = _ext.bmm
+    conv2d = _ext.conv2d
     plan = _ext.plan
     version = _ext.version
     extension_path = _ext.__file__

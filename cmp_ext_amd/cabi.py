@@ -26,6 +26,7 @@ SIGNATURES = {
     "cmpext3_matmul_fp32": (_i, [_p, _p, _p, _i, _i, _i, _p]),
     "cmpext3_gemm_ex": (_i, [_i, _i, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p,
                              _i, _i, _i, _i, _p, _i64, _p]),
+    "cmpext3_conv2d_1x1": (_i, [_i, _p, _p, _p, _p, _i, _i, _i, _i, _p, _i64, _p]),
     "cmpext3_gemm_workspace_size": (_i64, [_i, _i, _i, _i, _i, _i]),
     "cmpext3_gemm_plan": (_i, [_i, _i, _i, _i, _i, _i64, _i64, _i64, _i, _i, _i, _i64, _cp, _i]),
     "cmpext3_status_string": (_cp, [_i]),
@@ -88,6 +89,18 @@ def gemm_ex(dtype: int, layout: int, A, lda: int, stride_a: int, B, ldb: int, st
     return lib().cmpext3_gemm_ex(dtype, layout, ptr(A), lda, stride_a, ptr(B), ldb, stride_b, ptr(C),
                                  ldc, stride_c, ptr(bias), M, N, K, batch, ptr(workspace), ws_bytes,
                                  _stream_handle(stream))
+
+
+def conv2d_1x1(dtype: int, inp, weight, bias, out, batch: int, c_in: int, c_out: int, hw: int,
+               workspace=None, stream=None) -> int:
+    """Call cmpext3_conv2d_1x1 (contiguous NCHW input/output, [c_out, c_in] weight)."""
+    def ptr(x):
+        if x is None:
+            return None
+        return x.data_ptr() if hasattr(x, "data_ptr") else int(x)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    return lib().cmpext3_conv2d_1x1(dtype, ptr(inp), ptr(weight), ptr(bias), ptr(out), batch, c_in, c_out,
+                                    hw, ptr(workspace), ws_bytes, _stream_handle(stream))
 
 
 def matmul(dtype: int, A, B, C, M: int, N: int, K: int, stream=None) -> int:

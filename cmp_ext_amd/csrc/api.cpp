@@ -54,12 +54,11 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
 
 constexpr int64_t kMaxGridZ = 65535;
 
-}  // namespace
-
-extern "C" int cmpext3_gemm_ex(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride_a,
-                               const void* B, int64_t ldb, int64_t stride_b, void* C, int64_t ldc,
-                               int64_t stride_c, const void* bias, int M, int N, int K, int batch,
-                               void* workspace, int64_t workspace_bytes, void* stream) {
+// Shared body of cmpext3_gemm_ex (bias per column) and cmpext3_conv2d_1x1
+// (bias per row).
+int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb,
+             int64_t stride_b, void* C, int64_t ldc, int64_t stride_c, const void* bias, int bias_row, int M, int N,
+             int K, int batch, void* workspace, int64_t workspace_bytes, void* stream) {
   Request r{};
   r.dtype = dtype;
   r.layout = b_layout;
@@ -85,6 +84,7 @@ extern "C" int cmpext3_gemm_ex(int dtype, int b_layout, const void* A, int64_t l
   const int64_t esz = dtype == kF32 ? 4 : 2;
   GemmParams p{};
   p.bias = bias;
+  p.bias_row = bias_row;
   p.lda = lda;
   p.ldb = ldb;
   p.ldc = ldc;
@@ -108,6 +108,27 @@ extern "C" int cmpext3_gemm_ex(int dtype, int b_layout, const void* A, int64_t l
     if (e != hipSuccess) return (int)e;
   }
   return CMPEXT3_OK;
+}
+
+}  // namespace
+
+extern "C" int cmpext3_gemm_ex(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride_a,
+                               const void* B, int64_t ldb, int64_t stride_b, void* C, int64_t ldc,
+                               int64_t stride_c, const void* bias, int M, int N, int K, int batch,
+                               void* workspace, int64_t workspace_bytes, void* stream) {
+  return run_gemm(dtype, b_layout, A, lda, stride_a, B, ldb, stride_b, C, ldc, stride_c, bias, 0, M, N, K, batch,
+                  workspace, workspace_bytes, stream);
+}
+
+// NCHW 1x1 convolution = `batch` GEMMs out_b[c_out, hw] = W[c_out, c_in] * in_b[c_in, hw]
+// that share A (stride_a = 0), with B in the [K, N] layout and the bias per row.
+extern "C" int cmpext3_conv2d_1x1(int dtype, const void* input, const void* weight, const void* bias, void* output,
+                                  int batch, int c_in, int c_out, int hw, void* workspace, int64_t workspace_bytes,
+                                  void* stream) {
+  if (batch < 0 || c_in < 0 || c_out < 0 || hw < 0) return CMPEXT3_ERR_INVALID_ARG;
+  return run_gemm(dtype, CMPEXT3_B_KN, weight, c_in > 1 ? c_in : 1, 0, input, hw > 1 ? hw : 1, (int64_t)c_in * hw,
+                  output, hw > 1 ? hw : 1, (int64_t)c_out * hw, bias, 1, c_out, hw, c_in, batch, workspace,
+                  workspace_bytes, stream);
 }
 
 extern "C" int cmpext3_matmul_fp16(const void* A, const void* B, void* C, int M, int N, int K, void* stream) {

@@ -187,7 +187,8 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(const GemmParams p) {
   // acc[i][j][e] = C[m0 + wm*WTM + 16i + r16][n0 + wn*WTN + 16j + 4g + e]; elements
   // outside C get an out-of-range offset and are dropped by the store.
   const __amdgpu_buffer_rsrc_t crs = make_rsrc((float*)p.C + bz * p.stride_c + (int64_t)m0 * p.ldc + n0);
-  const float* bias = (const float*)p.bias;
+  const float* bias = p.bias_row ? nullptr : (const float*)p.bias;    // per column
+  const float* rbias = p.bias_row ? (const float*)p.bias : nullptr;   // per row
   float bv[FN][4];
 #pragma unroll
   for (int j = 0; j < FN; ++j)
@@ -200,13 +201,15 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(const GemmParams p) {
   for (int i = 0; i < FM; ++i) {
     const int row = wm * S::WTM + i * 16 + r16;
     const bool row_ok = m0 + row < M;
+    const float bm = (rbias != nullptr && row_ok) ? rbias[m0 + row] : 0.f;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int col = wn * S::WTN + j * 16 + 4 * g;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const bool ok = row_ok && n0 + col + e < N;
-        const float x = bias != nullptr ? acc[i][j][e] + bv[j][e] : acc[i][j][e];
+        const float x = bias != nullptr ? acc[i][j][e] + bv[j][e]
+                        : rbias != nullptr ? acc[i][j][e] + bm : acc[i][j][e];
         buf_store4(crs, ok ? (uint32_t)(row * p.ldc + col + e) * 4u : kBufOOB, x);
       }
     }

@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(const GemmParams p) {
       for (int e = 0; e < 4; ++e) {
         if (n + e < N) {
           float x = acc[i][j][e];
-          if (bias) x += from_bits<T>(bias[n + e]);
+          if (bias) x += from_bits<T>(bias[p.bias_row ? m : n + e]);
           crow[n + e] = to_bits<T>(x);
         }
       }

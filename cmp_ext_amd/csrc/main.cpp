@@ -189,6 +189,77 @@ torch::Tensor bmm(torch::Tensor input, torch::Tensor mat2) {
   return out;
 }
 
+// stride / padding / dilation as the reference parses them (src/main.cpp:140-148):
+// an int means the same value for H and W, otherwise a sequence of ints.
+std::vector<int64_t> expand_param(const py::object& v) {
+  if (py::isinstance<py::int_>(v)) {
+    const int64_t x = v.cast<int64_t>();
+    return {x, x};
+  }
+  std::vector<int64_t> r = v.cast<std::vector<int64_t>>();
+  TORCH_CHECK(!r.empty(), "cmpext3.conv2d: stride, padding and dilation need at least one value");
+  return r;
+}
+
+// conv2d(input[B, C_in, H, W], weight[C_out, C_in, 1, 1], bias[C_out]) -> [B, C_out, H, W]
+// Reference: custom_conv2d_forward, src/main.cpp:363-424 (checks :372-388, the
+// 1x1 branch :402-424).  The reference runs that branch as permute to NHWC +
+// linear on a contiguous copy + permute back into a second copy; here every
+// image is one GEMM out_b = W * in_b on the NCHW data as it lies, with the
+// bias added per output channel in the epilogue, all images in one launch.
+// The reference's general direct-convolution kernels (launch_conv2d_*, :458-488)
+// are not part of this library: any other kernel size, stride, padding or
+// dilation raises.
+torch::Tensor conv2d(torch::Tensor input, torch::Tensor weight, c10::optional<torch::Tensor> bias,
+                     const py::object& stride, const py::object& padding, const py::object& dilation,
+                     int64_t groups) {
+  TORCH_CHECK(input.dim() == 4, "Input must be 4D (NCHW)");
+  TORCH_CHECK(weight.dim() == 4, "Weight must be 4D (O I/G kH kW)");
+  TORCH_CHECK(input.device() == weight.device(), "Device mismatch");
+  TORCH_CHECK(groups == 1, "Currently only groups=1 is supported in this custom op");
+  TORCH_CHECK(input.size(1) == weight.size(1), "Input channels mismatch weight channels");
+  const std::vector<int64_t> s = expand_param(stride), pd = expand_param(padding), dl = expand_param(dilation);
+  const int64_t s_h = s[0], s_w = s.size() > 1 ? s[1] : s[0];
+  const int64_t p_h = pd[0], p_w = pd.size() > 1 ? pd[1] : pd[0];
+  const int64_t d_h = dl[0], d_w = dl.size() > 1 ? dl[1] : dl[0];
+  const int64_t kH = weight.size(2), kW = weight.size(3);
+  TORCH_CHECK(kH == 1 && kW == 1 && s_h == 1 && s_w == 1 && p_h == 0 && p_w == 0 && d_h == 1 && d_w == 1,
+              "cmpext3.conv2d: only the 1x1 kernel with stride 1, padding 0 and dilation 1 is provided "
+              "(it runs on the GEMM path); got kernel ", kH, "x", kW, ", stride (", s_h, ", ", s_w,
+              "), padding (", p_h, ", ", p_w, "), dilation (", d_h, ", ", d_w, ")");
+  TORCH_CHECK(input.scalar_type() == weight.scalar_type(), "Dtype mismatch");
+  const int code = dtype_code(input.scalar_type());
+  TORCH_CHECK(code >= 0, "Unsupported dtype for custom_conv2d");
+  TORCH_CHECK(input.is_cuda(), "cmpext3.conv2d: tensors must be on a GPU");
+  const int64_t Bn = input.size(0), Cin = input.size(1), H = input.size(2), W = input.size(3);
+  const int64_t Cout = weight.size(0);
+  checked_int(Bn, "batch");
+  checked_int(Cin, "C_in");
+  checked_int(Cout, "C_out");
+  const int64_t hw = checked_int(H * W, "H*W");
+  c10::DeviceGuard guard(input.device());
+  input = input.contiguous();
+  weight = weight.contiguous();
+  const void* bias_ptr = nullptr;
+  torch::Tensor bias_c;
+  if (bias.has_value() && bias->defined()) {
+    bias_c = *bias;
+    TORCH_CHECK(bias_c.device() == input.device(), "Bias device mismatch");
+    TORCH_CHECK(bias_c.scalar_type() == input.scalar_type(), "Bias dtype mismatch");
+    TORCH_CHECK(bias_c.dim() == 1, "Bias must be 1D");
+    TORCH_CHECK(bias_c.size(0) == Cout, "Bias size mismatch");
+    bias_c = bias_c.contiguous();
+    bias_ptr = bias_c.data_ptr();
+  }
+  torch::Tensor out = torch::empty({Bn, Cout, H, W}, input.options());
+  const torch::Tensor ws = workspace_for(code, CMPEXT3_B_KN, Cout, hw, Cin, Bn, input);
+  const int st = cmpext3_conv2d_1x1(code, input.data_ptr(), weight.data_ptr(), bias_ptr, out.data_ptr(), (int)Bn,
+                                    (int)Cin, (int)Cout, (int)hw, ws.defined() ? ws.data_ptr() : nullptr,
+                                    ws.defined() ? ws.numel() : 0, current_stream(input));
+  check_status(st, "conv2d");
+  return out;
+}
+
 std::string plan(const std::string& dtype, int64_t M, int64_t N, int64_t K, const std::string& layout,
                  int64_t batch, bool has_bias) {
   int code = dtype == "f16" || dtype == "fp16" ? CMPEXT3_F16
@@ -216,6 +287,9 @@ PYBIND11_MODULE(_cmpext3, m) {
   m.def("linear", &linear, "Custom linear layer implementation", py::arg("input"), py::arg("weight"),
         py::arg("bias") = py::none());
   m.def("bmm", &bmm, "Custom Batch Matrix Multiplication", py::arg("input"), py::arg("mat2"));
+  m.def("conv2d", &conv2d, "Custom conv2d layer (1x1, stride 1, padding 0: runs as a GEMM)", py::arg("input"),
+        py::arg("weight"), py::arg("bias") = py::none(), py::arg("stride") = 1, py::arg("padding") = 0,
+        py::arg("dilation") = 1, py::arg("groups") = 1);
   m.def("plan", &plan, "Describe the kernel chosen for a GEMM shape", py::arg("dtype"), py::arg("M"),
         py::arg("N"), py::arg("K"), py::arg("layout") = "KN", py::arg("batch") = 1,
         py::arg("has_bias") = false);

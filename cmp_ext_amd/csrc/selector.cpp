@@ -117,7 +117,9 @@ int make_plan(const Request& r, Plan* plan) {
       const int64_t chunk = std::min<int64_t>(r.batch, 65535);
       const int64_t strips = cdiv(r.N, 128);
       int64_t splits = 1;
-      if (strips * chunk < 192) splits = std::min<int64_t>(8, std::max<int64_t>(1, 256 / (strips * chunk)));
+      // (empty problems -- N or batch 0 -- launch nothing; keep the arithmetic defined)
+      const int64_t wgs1 = std::max<int64_t>(1, strips * chunk);
+      if (wgs1 < 192) splits = std::min<int64_t>(8, std::max<int64_t>(1, 256 / wgs1));
       splits = std::min<int64_t>(splits, std::max<int64_t>(1, r.K / 256));
       const int64_t need = splits > 1 ? splits * chunk * r.M * r.N * 4 : 0;
       const int64_t wide_wgs = strips * splits * chunk, narrow_wgs = cdiv(r.N, 32) * chunk;

@@ -183,7 +183,7 @@ __global__ void __launch_bounds__(256) gemm_skinny_narrow_kernel(const GemmParam
     float s = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) s += red[(w * MB * 16 + row) * kSkinnyStrip + col];
-    if (bias) s += from_bits<T>(bias[n]);
+    if (bias) s += from_bits<T>(bias[p.bias_row ? row : n]);
     ((uint16_t*)(Cb + (int64_t)row * p.ldc))[n] = to_bits<T>(s);
   }
 }

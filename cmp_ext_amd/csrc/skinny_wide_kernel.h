@@ -173,7 +173,7 @@ __global__ void __launch_bounds__(256) gemm_skinny_wide_kernel(const GemmParams 
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float x = acc[h][mb][r];
-          if (bias) x += from_bits<T>(bias[n + r]);
+          if (bias) x += from_bits<T>(bias[p.bias_row ? m : n + r]);
           crow[n + r] = to_bits<T>(x);
         }
       } else {
@@ -205,7 +205,7 @@ __global__ void __launch_bounds__(256) skinny_reduce_kernel(const GemmParams p, 
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     float x = s[r];
-    if (bias) x += from_bits<T>(bias[n + r]);
+    if (bias) x += from_bits<T>(bias[p.bias_row ? m : n + r]);
     crow[n + r] = to_bits<T>(x);
   }
 }

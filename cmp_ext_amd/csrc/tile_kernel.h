@@ -315,12 +315,14 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmPa
   // ---- epilogue: register 4q..4q+3 of block (i, j) is C[m][n..n+3] with
   // m = 32i + lane%32 and n = 32j + 8q + 4*(lane/32) ----
   T* Cb = (T*)p.C + bz * p.stride_c;
-  const T* bias = (const T*)p.bias;
+  const T* bias = p.bias_row ? nullptr : (const T*)p.bias;      // per column
+  const uint16_t* rbias = p.bias_row ? (const uint16_t*)p.bias : nullptr;  // per row
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int m = m0 + wm * S::WTM + i * 32 + r32;
     if (m >= M) continue;
     T* crow = Cb + (int64_t)m * p.ldc;
+    const float bm = rbias ? from_bits<T>(rbias[m]) : 0.f;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
 #pragma unroll
@@ -328,6 +330,10 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmPa
         const int n = n0 + wn * S::WTN + j * 32 + 8 * q + 4 * h;
         if (n >= N) continue;
         float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        if (rbias) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] += bm;
+        }
         if (n + 4 <= N) {
           if (bias) {
             const u32x2 bb = *(const u32x2*)(bias + n);

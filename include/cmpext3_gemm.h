@@ -86,6 +86,26 @@ int cmpext3_gemm_ex(int dtype, int b_layout,
                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * 1x1 convolution with stride 1, padding 0, dilation 1 and groups 1 on
+ * contiguous NCHW tensors:
+ *   output[b][o][p] = sum_c weight[o][c] * input[b][c][p] (+ bias[o])
+ * with input [batch, c_in, hw], weight [c_out, c_in] (the [c_out, c_in, 1, 1]
+ * tensor), bias NULL or [c_out], output [batch, c_out, hw], hw = H * W, all of
+ * one dtype.  Each image is one GEMM out_b[c_out, hw] = W * in_b[c_in, hw]
+ * (A = the weight, shared; B = the image in the [K, N] layout; the bias added
+ * per output row), all images in one launch.  `workspace` is as for
+ * cmpext3_gemm_ex; cmpext3_gemm_workspace_size(dtype, CMPEXT3_B_KN, c_out,
+ * hw, c_in, batch) says how much helps.
+ * Replaces the 1x1 branch of custom_conv2d_forward (src/main.cpp:402-424),
+ * which permutes NCHW to NHWC, runs custom_linear_forward on a contiguous
+ * copy (with its weight transpose copy and separate bias kernel) and permutes
+ * the result back into a second copy; here no copy is made.
+ */
+int cmpext3_conv2d_1x1(int dtype, const void* input, const void* weight, const void* bias, void* output,
+                       int batch, int c_in, int c_out, int hw,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Bytes of workspace cmpext3_gemm_ex can use for these arguments (packed
  * operands, 16-byte aligned); 0 when the chosen kernel needs none, or a
  * negative CMPEXT3_ERR_*.  Host only.  No counterpart in the reference, whose

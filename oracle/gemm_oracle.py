@@ -12,6 +12,10 @@ What it restates (eastmoe/cmp_ext, read as text, never run):
     output shaped [..., N] -- custom_linear_forward (src/main.cpp:155-256).
   * bmm(input[B, M, K], mat2[B, K, N]) = per-batch matmul --
     custom_bmm_forward (src/main.cpp:273-357).
+  * conv2d with a 1x1 kernel, stride 1, padding 0, dilation 1, groups 1:
+    NCHW -> NHWC, linear with the [C_out, C_in] view of the weight (+ bias),
+    NHWC -> NCHW -- the 1x1 branch of custom_conv2d_forward
+    (src/main.cpp:402-424).
 The reference accumulates fp16/bf16 products in half precision
 (fp16_matmul.cu:86-98, bf16_matmul.cu:65-77); the operator contract this
 build implements (fp32 accumulation, one final rounding to the input dtype)
@@ -22,7 +26,9 @@ Pinning (tests/test_oracle.py): matmul_f64 is checked against an exactly
 rounded dot product per element (math.fsum of exact float64 products, via the
 committed golden fixtures and directly), against the plain-C triple loop in
 oracle/gemm_ref.c, and against closed forms (identity, permutation, zero,
-rank-1 integer, K = 1, transpose and linearity identities).  The dtype
+rank-1 integer, K = 1, transpose and linearity identities).  conv2d_1x1_f64
+is checked against exactly rounded golden values, against
+torch.nn.functional.conv2d in float64 and against matmul_f64 per image.  The dtype
 rounding functions are checked against IEEE bit-level decoding in C and
 against exhaustive/boundary cases.
 """
@@ -99,6 +105,21 @@ def bmm_f64(a: np.ndarray, b: np.ndarray) -> np.ndarray:
         raise ValueError("bmm: bad shapes")
     return np.stack([matmul_f64(a[i], b[i]) for i in range(a.shape[0])]) if a.shape[0] else \
         np.zeros((0, a.shape[1], b.shape[2]))
+
+
+def conv2d_1x1_f64(x: np.ndarray, w: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+    """1x1 convolution as the reference computes it (src/main.cpp:402-424):
+    input [B, C_in, H, W] permuted to NHWC (:407), linear against the weight
+    viewed as [C_out, C_in] (:410, :418), result permuted back to
+    [B, C_out, H, W] (:423)."""
+    x = np.asarray(x, dtype=np.float64)
+    w = np.asarray(w, dtype=np.float64)
+    if x.ndim != 4 or w.ndim != 4 or w.shape[2:] != (1, 1) or x.shape[1] != w.shape[1]:
+        raise ValueError("conv2d_1x1: bad shapes")
+    nhwc = np.transpose(x, (0, 2, 3, 1))
+    out = linear_f64(nhwc, w.reshape(w.shape[0], w.shape[1]), bias) if x.shape[1] else \
+        np.zeros(nhwc.shape[:3] + (w.shape[0],)) + (0 if bias is None else np.asarray(bias, np.float64))
+    return np.ascontiguousarray(np.transpose(out, (0, 3, 1, 2)))
 
 
 def rel_frobenius(out: np.ndarray, ref: np.ndarray) -> float:

@@ -36,6 +36,14 @@ CASES = {
 }
 
 
+# 1x1 convolutions: name: (dtype, batch, c_in, H, W, c_out, with_bias, seed)
+CONV_CASES = {
+    "conv_f16_2x5x3x4_o6_bias": ("fp16", 2, 5, 3, 4, 6, True, 21),
+    "conv_bf16_3x24x2x5_o7": ("bf16", 3, 24, 2, 5, 7, False, 22),
+    "conv_f32_1x9x4x4_o3_bias": ("fp32", 1, 9, 4, 4, 3, True, 23),
+}
+
+
 def bits(t) -> np.ndarray:
     import torch
 
@@ -71,6 +79,26 @@ def main() -> None:
             exp = np.array([[math.fsum([exp[m, n], bb[n]]) for n in range(N)] for m in range(M)])
         data[name + "/a"] = bits(a)
         data[name + "/b"] = bits(b)
+        data[name + "/expected"] = exp
+    for name, (dt, B, C, H, W, O, with_bias, seed) in CONV_CASES.items():
+        tdt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dt]
+        g = torch.Generator().manual_seed(seed)
+        x = (torch.rand((B, C, H, W), generator=g) * 2 - 1).to(tdt)
+        w = (torch.rand((O, C, 1, 1), generator=g) * 2 - 1).to(tdt)
+        bias = (torch.rand((O,), generator=g) * 2 - 1).to(tdt) if with_bias else None
+        xf, wf = to_f64(x), to_f64(w)
+        bf = to_f64(bias) if with_bias else np.zeros(O)
+        exp = np.zeros((B, O, H, W))
+        for b_ in range(B):
+            for o in range(O):
+                for h in range(H):
+                    for w_ in range(W):
+                        terms = [float(xf[b_, c, h, w_]) * float(wf[o, c, 0, 0]) for c in range(C)]
+                        exp[b_, o, h, w_] = math.fsum(terms + ([float(bf[o])] if with_bias else []))
+        data[name + "/x"] = bits(x)
+        data[name + "/w"] = bits(w)
+        if with_bias:
+            data[name + "/bias"] = bits(bias)
         data[name + "/expected"] = exp
     # fingerprints of the benchmark inputs (seed 0): first 8 elements of A and
     # of B, and float64 sums of each, as produced by the seeded generator

@@ -7,7 +7,7 @@ import cmpext3
 
 
 def test_module_surface():
-    for name in ["fp16_matmul", "bf16_matmul", "fp32_matmul", "linear", "bmm", "plan", "version"]:
+    for name in ["fp16_matmul", "bf16_matmul", "fp32_matmul", "linear", "bmm", "conv2d", "plan", "version"]:
         assert callable(getattr(cmpext3, name))
     assert "gfx950" in cmpext3.version()
     assert cmpext3.extension_path.endswith(".so")
@@ -55,3 +55,30 @@ def test_linear_and_bmm_argument_checks():
         cmpext3.bmm(x, torch.zeros(2, 7, 2, dtype=torch.float16))
     with pytest.raises(RuntimeError, match="Dtype mismatch"):
         cmpext3.bmm(x, torch.zeros(2, 8, 2, dtype=torch.float32))
+
+
+def test_conv2d_argument_checks():
+    """The reference's conv2d checks (src/main.cpp:372-388) in the same order,
+    then the 1x1 / stride 1 / padding 0 / dilation 1 restriction of this
+    library, all before any GPU work."""
+    x = torch.zeros(2, 8, 5, 5, dtype=torch.float16)
+    w = torch.zeros(4, 8, 1, 1, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="Input must be 4D"):
+        cmpext3.conv2d(x[0], w)
+    with pytest.raises(RuntimeError, match="Weight must be 4D"):
+        cmpext3.conv2d(x, w[:, :, 0, 0])
+    with pytest.raises(RuntimeError, match="only groups=1"):
+        cmpext3.conv2d(x, w, groups=2)
+    with pytest.raises(RuntimeError, match="Input channels mismatch"):
+        cmpext3.conv2d(x, torch.zeros(4, 7, 1, 1, dtype=torch.float16))
+    for kw in (dict(stride=2), dict(stride=(1, 2)), dict(padding=1), dict(padding=[0, 1]), dict(dilation=2)):
+        with pytest.raises(RuntimeError, match="only the 1x1 kernel"):
+            cmpext3.conv2d(x, w, **kw)
+    with pytest.raises(RuntimeError, match="only the 1x1 kernel"):
+        cmpext3.conv2d(x, torch.zeros(4, 8, 3, 3, dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="Dtype mismatch"):
+        cmpext3.conv2d(x, w.float())
+    with pytest.raises(RuntimeError, match="Unsupported dtype"):
+        cmpext3.conv2d(x.double(), w.double())
+    with pytest.raises(RuntimeError, match="on a GPU"):
+        cmpext3.conv2d(x, w, stride=(1, 1), padding=(0, 0), dilation=[1])   # sequences accepted; CPU rejected

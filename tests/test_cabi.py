@@ -69,6 +69,13 @@ def test_empty_problems_launch_nothing():
     assert lib.cmpext3_gemm_ex(cabi.BF16, cabi.B_NK, None, 8, 0, None, 8, 0, None, 8, 0, None, 8, 8, 8, 0, None, 0,
                                None) == 0
     assert lib.cmpext3_matmul_fp16(None, None, None, 0, 0, 0, None) == 0
+    # skinny-M shapes with no columns or no batch entries (the split-K planner divides by both)
+    assert lib.cmpext3_gemm_ex(cabi.F16, cabi.B_KN, None, 8, 0, None, 8, 0, None, 8, 0, None, 8, 0, 8, 1, None, 0,
+                               None) == 0
+    assert lib.cmpext3_gemm_ex(cabi.F16, cabi.B_KN, None, 8, 0, None, 8, 0, None, 8, 0, None, 8, 8, 8, 0, None, 0,
+                               None) == 0
+    assert cabi.workspace_size(cabi.F16, cabi.B_KN, 16, 0, 8192) == 0
+    assert cabi.workspace_size(cabi.BF16, cabi.B_KN, 16, 8192, 8192, batch=0) == 0
 
 
 def test_workspace_size_query():
@@ -78,3 +85,20 @@ def test_workspace_size_query():
     assert cabi.workspace_size(cabi.F32, cabi.B_KN, 16, 8192, 8192) == 0
     assert cabi.workspace_size(cabi.F16, cabi.B_KN, 16, 32768, 4096) == 0    # enough strips: no split
     assert cabi.workspace_size(7, cabi.B_KN, 16, 64, 64) == cabi.ERR_UNSUPPORTED
+
+
+def test_conv2d_1x1_rejects_and_empty():
+    lib = cabi.lib()
+    # negative sizes and unknown dtypes are rejected before any launch
+    assert lib.cmpext3_conv2d_1x1(cabi.F16, 0x1000, 0x2000, None, 0x3000, -1, 8, 8, 64, None, 0, None) == \
+        cabi.ERR_INVALID_ARG
+    assert lib.cmpext3_conv2d_1x1(cabi.F16, 0x1000, 0x2000, None, 0x3000, 1, 8, -8, 64, None, 0, None) == \
+        cabi.ERR_INVALID_ARG
+    assert lib.cmpext3_conv2d_1x1(5, 0x1000, 0x2000, None, 0x3000, 1, 8, 8, 64, None, 0, None) == \
+        cabi.ERR_UNSUPPORTED
+    assert lib.cmpext3_conv2d_1x1(cabi.F32, 0x1000, 0x2000, None, None, 1, 8, 8, 64, None, 0, None) == \
+        cabi.ERR_INVALID_ARG                                         # null output with work to do
+    # empty batch / no pixels / no output channels: success, nothing touched
+    assert lib.cmpext3_conv2d_1x1(cabi.F16, None, None, None, None, 0, 8, 8, 64, None, 0, None) == cabi.OK
+    assert lib.cmpext3_conv2d_1x1(cabi.BF16, None, None, None, None, 2, 8, 8, 0, None, 0, None) == cabi.OK
+    assert lib.cmpext3_conv2d_1x1(cabi.F32, None, None, None, None, 2, 8, 0, 64, None, 0, None) == cabi.OK

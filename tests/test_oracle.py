@@ -222,3 +222,73 @@ def test_cfg1_cpu_reference_path_within_fp32_bound():
     assert 0.0 < err <= O.TOLERANCE["fp32"]
     # A planted mistake (operand transposed) is far outside the bound.
     assert O.reference_check(O.cpu_matmul(a, b.T.contiguous()), a, b, "fp32") > 0.5
+
+
+# ---- conv2d 1x1 (the reference runs it through linear, src/main.cpp:402-424) ----
+
+CONV_CASES = ["conv_f16_2x5x3x4_o6_bias", "conv_bf16_3x24x2x5_o7", "conv_f32_1x9x4x4_o3_bias"]
+
+
+def conv_operands(golden, name):
+    dt = {"f16": "fp16", "bf16": "bf16", "f32": "fp32"}[name.split("_")[1]]
+    exp = golden[name + "/expected"]
+    B, O_, H, W = exp.shape
+    x = decode(golden[name + "/x"], dt).reshape(B, -1, H, W)
+    w = decode(golden[name + "/w"], dt).reshape(O_, -1, 1, 1)
+    bias = decode(golden[name + "/bias"], dt) if name + "/bias" in golden else None
+    return x, w, bias, exp
+
+
+@pytest.mark.parametrize("name", CONV_CASES)
+def test_conv_oracle_matches_exactly_rounded_golden(golden, name):
+    x, w, bias, exp = conv_operands(golden, name)
+    out = O.conv2d_1x1_f64(x, w, bias)
+    assert out.shape == exp.shape
+    scale = np.einsum("bchw,oc->bohw", np.abs(x), np.abs(w[:, :, 0, 0])) + \
+        (np.abs(bias)[None, :, None, None] if bias is not None else 0)
+    assert np.all(np.abs(out - exp) <= 1e-14 * scale + 1e-300)
+
+
+@pytest.mark.parametrize("B,C,H,W,Co", [(1, 1, 1, 1, 1), (2, 3, 5, 7, 4), (3, 16, 4, 1, 9), (1, 0, 2, 2, 3)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_conv_oracle_matches_torch_conv2d_and_per_image_matmul(B, C, H, W, Co, with_bias):
+    rng = np.random.default_rng(B * 1000 + C * 100 + H * 10 + W + Co)
+    x = rng.standard_normal((B, C, H, W))
+    w = rng.standard_normal((Co, C, 1, 1))
+    bias = rng.standard_normal(Co) if with_bias else None
+    out = O.conv2d_1x1_f64(x, w, bias)
+    if C > 0:   # (torch returns no output channels at all for C_in = 0; the empty sum is 0 + bias)
+        ref = torch.nn.functional.conv2d(torch.from_numpy(x), torch.from_numpy(w),
+                                         None if bias is None else torch.from_numpy(bias)).numpy()
+        np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12 * max(C, 1))
+    else:
+        np.testing.assert_array_equal(out, np.zeros((B, Co, H, W)) + (0 if bias is None else bias[None, :, None, None]))
+    for b in range(B):   # each image is the GEMM W[Co, C] @ X_b[C, H*W] (+ bias per row)
+        mm = O.matmul_f64(w[:, :, 0, 0], x[b].reshape(C, H * W))
+        if bias is not None:
+            mm = mm + bias[:, None]
+        np.testing.assert_allclose(out[b].reshape(Co, H * W), mm, rtol=1e-12, atol=1e-12 * max(C, 1))
+
+
+def _conv_wrong_permute(x, w, bias):   # NHWC built as N,W,H,C and not undone
+    out = O.linear_f64(np.transpose(x, (0, 3, 2, 1)), w[:, :, 0, 0], bias)
+    return np.transpose(out, (0, 3, 1, 2))
+
+
+def _conv_bias_per_column(x, w, bias):  # bias indexed by pixel instead of channel
+    out = O.conv2d_1x1_f64(x, w, None)
+    flat = out.reshape(out.shape[0], out.shape[1], -1)
+    n = flat.shape[2]
+    flat = flat + np.resize(bias, n)[None, None, :]
+    return flat.reshape(out.shape)
+
+
+def _conv_dropped_channel(x, w, bias):
+    return O.conv2d_1x1_f64(x[:, 1:], w[:, 1:], bias)
+
+
+@pytest.mark.parametrize("mutant", [_conv_wrong_permute, _conv_bias_per_column, _conv_dropped_channel])
+def test_conv_planted_mistakes_are_caught(golden, mutant):
+    x, w, bias, exp = conv_operands(golden, "conv_f16_2x5x3x4_o6_bias")
+    out = mutant(x, w, bias)
+    assert out.shape != exp.shape or O.rel_frobenius(out, exp) > O.TOLERANCE["fp16"]
