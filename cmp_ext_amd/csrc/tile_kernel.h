@@ -244,12 +244,14 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmPa
   };
   // One sub-step (16 k) of MFMAs on fragment buffer `buf`, with the reads of
   // the next sub-step's fragments (into the other buffer) spread over its
-  // first three quarters and DMA pieces [d0, d1) of step `dkt` spread evenly:
+  // MFMA slots (all 16 of a 128x128 wave block; the first three quarters of
+  // smaller blocks, whose last reads would otherwise land too late) and DMA
+  // pieces [d0, d1) of step `dkt` spread evenly:
   // short bursts keep the per-CU address FIFOs and the LDS queue from
   // filling, which would stall the MFMA issue behind them.  A scheduling
   // barrier after every MFMA slot keeps the compiler from regrouping them.
   constexpr int X = FM * FN;
-  constexpr int XR = (3 * X + 3) / 4;  // MFMA slots that carry reads
+  constexpr int XR = X >= 16 ? X : (3 * X + 3) / 4;  // MFMA slots that carry reads
   auto substep = [&](int buf, int rkt, int rks, int d0, int d1, int dkt) {
 #pragma unroll
     for (int x = 0; x < X; ++x) {
@@ -312,46 +314,69 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_tile_kernel(const GemmPa
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // no LDS DMA may outlive the workgroup
   }
 
-  // ---- epilogue: register 4q..4q+3 of block (i, j) is C[m][n..n+3] with
-  // m = 32i + lane%32 and n = 32j + 8q + 4*(lane/32) ----
+  // ---- epilogue.  Register 4q+e of block (i, j) is C[m][n] with m = 32i + lane%32 and
+  // n = 32j + 8q + 4h + e (h = lane/32): four consecutive columns per lane.
+  // After rounding to 16-bit pairs, one v_permlane32_swap per dword trades
+  // q = 1 of the lower half-wave for q = 0 of the upper half (and q = 3 for
+  // q = 2), so every lane holds 8 consecutive columns, n = 32j + 16pp + 8h + 0..7
+  // (pp = 0, 1), and C is written with 16-byte stores: half as many store
+  // instructions as 8-byte pieces, which is what bounds this tail. ----
   T* Cb = (T*)p.C + bz * p.stride_c;
-  const T* bias = p.bias_row ? nullptr : (const T*)p.bias;      // per column
+  const uint16_t* cbias = p.bias_row ? nullptr : (const uint16_t*)p.bias;  // per column
   const uint16_t* rbias = p.bias_row ? (const uint16_t*)p.bias : nullptr;  // per row
+  const bool st16 = (p.ldc & 7) == 0;
+  const int mw = m0 + wm * S::WTM, nw = n0 + wn * S::WTN;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
-    const int m = m0 + wm * S::WTM + i * 32 + r32;
-    if (m >= M) continue;
-    T* crow = Cb + (int64_t)m * p.ldc;
-    const float bm = rbias ? from_bits<T>(rbias[m]) : 0.f;
+    const int m = mw + i * 32 + r32;
+    const float bm = (rbias != nullptr && m < M) ? from_bits<T>(rbias[m]) : 0.f;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
+      uint32_t P[4][2];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * S::WTN + j * 32 + 8 * q + 4 * h;
-        if (n >= N) continue;
-        float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e];
         if (rbias) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] += bm;
         }
-        if (n + 4 <= N) {
-          if (bias) {
-            const u32x2 bb = *(const u32x2*)(bias + n);
-            v[0] += from_bits<T>((uint16_t)(bb.x & 0xFFFF));
-            v[1] += from_bits<T>((uint16_t)(bb.x >> 16));
-            v[2] += from_bits<T>((uint16_t)(bb.y & 0xFFFF));
-            v[3] += from_bits<T>((uint16_t)(bb.y >> 16));
+        if (cbias) {
+          const int n = nw + j * 32 + 8 * q + 4 * h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) v[e] += from_bits<T>(cbias[n + e]);
+        }
+        P[q][0] = pack2<T>(v[0], v[1]);
+        P[q][1] = pack2<T>(v[2], v[3]);
+      }
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(P[2 * pp][w], P[2 * pp + 1][w], false, false);
+          P[2 * pp][w] = sw[0];
+          P[2 * pp + 1][w] = sw[1];
+        }
+      if (m >= M) continue;
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+        const int n = nw + j * 32 + 16 * pp + 8 * h;
+        if (n >= N) continue;
+        T* dst = Cb + (int64_t)m * p.ldc + n;
+        const u32x4 v = {P[2 * pp][0], P[2 * pp][1], P[2 * pp + 1][0], P[2 * pp + 1][1]};
+        if (n + 8 <= N) {
+          if (st16) {
+            *(u32x4*)dst = v;
+          } else {  // ldc % 8 == 4: 8-byte aligned rows
+            *(u32x2*)dst = u32x2{v.x, v.y};
+            *(u32x2*)(dst + 4) = u32x2{v.z, v.w};
           }
-          *(u32x2*)(crow + n) = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
         } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (n + e < N) {
-              float x = v[e];
-              if (bias) x += from_bits<T>(((const uint16_t*)bias)[n + e]);
-              ((uint16_t*)crow)[n + e] = to_bits<T>(x);
-            }
-          }
+          for (int e = 0; e < 8; ++e)
+            if (n + e < N) ((uint16_t*)dst)[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
         }
       }
     }
