@@ -109,6 +109,39 @@ def test_skinny(dtype, M, N, K):
     assert err_vs_oracle(c, a, b, dtype) <= O.TOLERANCE[dtype]
 
 
+def test_skinny_split_k_repeated_and_concurrent():
+    """Split-K skinny products (fp32 partials in the workspace, summed by a
+    second launch): many calls in a row, batched calls, and calls on two
+    streams at once, each with its own workspace, must all give the same bits
+    as the first call, and match the oracle."""
+    a, b = O.make_inputs("fp16", 16, 1024, 8192, "normal", 8192 ** -0.5, 3)
+    ag, bg = a.cuda(), b.cuda()
+    desc = cmpext3.plan("fp16", 16, 1024, 8192)
+    assert "skinny_wide" in desc and "splits=1 " not in desc, desc
+    ref = cmpext3.fp16_matmul(ag, bg)
+    torch.cuda.synchronize()
+    assert err_vs_oracle(ref, a, b, "fp16") <= O.TOLERANCE["fp16"]
+    mismatches = torch.zeros((), dtype=torch.int64, device="cuda")
+    for _ in range(2000):
+        mismatches += (cmpext3.fp16_matmul(ag, bg) != ref).sum()
+    assert mismatches.item() == 0
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(s1):
+        o1 = [cmpext3.fp16_matmul(ag, bg) for _ in range(50)]
+    with torch.cuda.stream(s2):
+        o2 = [cmpext3.fp16_matmul(ag, bg) for _ in range(50)]
+    torch.cuda.synchronize()
+    assert all(torch.equal(o, ref) for o in o1 + o2)
+    # batched: every batch entry has its own counters
+    a3 = torch.stack([ag, ag * 0.5, -ag])
+    b3 = torch.stack([bg, bg, bg * 2])
+    assert "splits=1 " not in cmpext3.plan("fp16", 16, 1024, 8192, batch=3)
+    o3 = cmpext3.bmm(a3, b3)
+    torch.cuda.synchronize()
+    for i in range(3):
+        assert err_vs_oracle(o3[i], a3[i], b3[i], "fp16") <= O.TOLERANCE["fp16"]
+
+
 @pytest.mark.parametrize("M,N,K,kernel", [(512, 512, 512, "f32tile64x64"), (65, 47, 3, "f32tile64x64"),
                                           (1, 1, 1, "f32tile64x64"), (6144, 8192, 64, "f32tile128x128"),
                                           (257, 131, 129, "f32tile64x64"),
