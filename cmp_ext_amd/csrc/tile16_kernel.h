@@ -1,0 +1,335 @@
+// Large-shape f16/bf16 GEMM for gfx950 on 16x16x32 matrix-core products:
+// C = A * op(B) (+ bias), fp32 accumulate.
+//
+// Counterpart of gemm_fp16_ampere_optimized_v3 (src/cuda/fp16_matmul.cu:63-283)
+// and gemm_bf16_kernel (src/cuda/bf16_matmul.cu:51-226): same contract (row-major
+// A[M,K], B[K,N], C[M,N]; zero-filled out-of-range loads, per-element masked
+// stores), built around the CDNA4 matrix cores and accumulating in fp32.
+//
+// Structure (one workgroup of 4 waves in a 2 x 2 grid = one BM x BN tile):
+//   * Each wave owns a (BM/2) x (BN/2) block of C as (BM/32) x (BN/32) blocks of
+//     16 x 16 fp32 accumulators (AGPRs), fed by v_mfma_f32_16x16x32_{f16,bf16}.
+//     A 16-wide block grain lets a 256 x 224 tile (the MLP shape) keep the
+//     2 x 2 wave grid; the 2 x 2 grid reads the fewest fragment bytes from LDS
+//     per MFMA.  Measured on MI355X, this kernel also holds a higher shader
+//     clock under the power limit than the same tile on 32x32x16 products.
+//   * K steps of BK = 64 go global -> LDS by buffer_load_dwordx4 ... lds (LDS
+//     DMA: no registers, no ds_write) into a two-stage ring.  A step is two
+//     sub-steps of 32 k.  All reads of a step's slot are issued by the end of its
+//     first sub-step (they fetch the second sub-step's fragments), so one barrier
+//     between the two sub-steps both frees slot t and certifies step t+1; the
+//     second sub-step then reads step t+1's first fragments and issues all of
+//     step t+2's DMA into slot t, which has a sub-step and a half to land before
+//     the next barrier.
+//   * A (and B given as [N,K]) are K-contiguous: LDS rows of 128 bytes in the
+//     lds_off128 layout, one ds_read_b128 per 16 x 32 fragment, conflict free.
+//   * B given as [K,N] stays [k][n] in LDS (rows padded to a multiple of 256
+//     bytes, 64-byte segments XORed with k%4) and is read with
+//     ds_read_b64_tr_b16, the CDNA4 transposing LDS read: two per fragment.
+//   * Out-of-range pieces (rows >= M, columns >= N, k >= K) use an offset past
+//     the buffer descriptor's range: the hardware writes zeros into LDS.
+//   * The reads of the next sub-step's fragments and the DMA pieces are spread
+//     one per MFMA slot, with a scheduling barrier after every slot.
+//   * Epilogue: fp32 -> T, bias added in fp32 first (per column, or per row);
+//     one v_permlane16_swap per dword pairs accumulator blocks j and j+1 so
+//     that every lane holds 8 consecutive columns, and C is written with
+//     16-byte stores covering 64 contiguous bytes of each of 16 rows.
+#pragma once
+
+#include <type_traits>
+#include <utility>
+
+#include "device_common.h"
+#include "tile_kernel.h"  // lds_off128, dma_kn_geom
+
+namespace cmpext3 {
+
+// f(std::integral_constant<int, I>) for I = 0 .. N-1, fully unrolled (register
+// arrays indexed by I stay in registers).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int BM, int BN, bool KN>
+struct Tile16Shape {
+  static constexpr int BK = 64;
+  static constexpr int ROW = BK * 2;  // bytes per LDS row of a K-contiguous operand
+  static constexpr int WTM = BM / 2, WTN = BN / 2;
+  static constexpr int FM = WTM / 16, FN = WTN / 16;
+  static constexpr int A_BYTES = BM * ROW;
+  static constexpr int B_PITCH = KN ? (BN * 2 + 255) / 256 * 256 : ROW;  // bytes per LDS row of B
+  static constexpr int B_BYTES = KN ? BK * B_PITCH : (BN + 63) / 64 * 64 * ROW;  // rows >= BN are OOB
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int LDS = 2 * STAGE;
+  static constexpr int A_DMA = A_BYTES / 1024 / 4;  // 1 KB LDS-DMA loads per wave per step
+  static constexpr int B_DMA = B_BYTES / 1024 / 4;
+  static constexpr int DMA = A_DMA + B_DMA;
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "16-row/column blocks");
+  static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "whole DMA loads per wave");
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+  static_assert(DMA <= 63, "vmcnt range");
+};
+
+// BIAS: 0 none, 1 per column of C (Linear), 2 per row (conv 1x1).  A kernel per
+// mode keeps the bias-free epilogue lean: the register allocator then keeps the
+// accumulators in AGPRs through the main loop.
+template <typename T, bool KN, int BM, int BN, int BIAS>
+__global__ void __launch_bounds__(256, 1) gemm_tile16_kernel(const GemmParams p) {
+  using S = Tile16Shape<BM, BN, KN>;
+  constexpr int FM = S::FM, FN = S::FN;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::LDS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int tm, tn;
+  tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int M = p.M, N = p.N, K = p.K;
+  const int64_t lda = p.lda, ldb = p.ldb;
+  const int64_t bz = blockIdx.z;
+  const T* Abase = (const T*)p.A + bz * p.stride_a + (int64_t)m0 * lda;
+  const T* Bbase = KN ? (const T*)p.B + bz * p.stride_b + n0 : (const T*)p.B + bz * p.stride_b + (int64_t)n0 * ldb;
+
+  // ---- per-lane DMA sources, relative to the step's first k; rows past the matrix are OOB ----
+  uint32_t a_off[S::A_DMA];
+  int a_kx[S::A_DMA];  // k offset of the lane's 16-byte piece within the step
+#pragma unroll
+  for (int i = 0; i < S::A_DMA; ++i) {
+    int row, chunk;
+    dma128_geom(wave * S::A_DMA + i, lane, row, chunk);
+    a_off[i] = (m0 + row < M) ? (uint32_t)(row * lda + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
+    a_kx[i] = 8 * chunk;
+  }
+  uint32_t b_off[S::B_DMA];
+  int b_kx[S::B_DMA];
+#pragma unroll
+  for (int i = 0; i < S::B_DMA; ++i) {
+    if (KN) {
+      int k, n;
+      dma_kn_geom(wave * S::B_DMA + i, lane, S::B_PITCH, k, n);
+      b_off[i] = (n < BN && n0 + n < N) ? (uint32_t)(k * ldb + n) * (uint32_t)sizeof(T) : kBufOOB;
+      b_kx[i] = k;
+    } else {
+      int row, chunk;
+      dma128_geom(wave * S::B_DMA + i, lane, row, chunk);
+      b_off[i] = (row < BN && n0 + row < N) ? (uint32_t)(row * ldb + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
+      b_kx[i] = 8 * chunk;
+    }
+  }
+  // LDS-DMA load d (A pieces first, then B) of K step kt into ring slot kt % 2;
+  // every k is checked against K, so steps at or past the end load zeros.
+  auto dma_piece = [&](int kt, int d) {
+    const int k0 = kt * S::BK;
+    const uint32_t sA = lds_addr(smem) + (uint32_t)((kt & 1) * S::STAGE);
+    const int krem = K - k0;
+    if (d < S::A_DMA) {
+      dma_load16(make_rsrc_sgpr(Abase + k0), a_kx[d] < krem ? a_off[d] : kBufOOB, sA + (wave * S::A_DMA + d) * 1024);
+    } else {
+      const int i = d - S::A_DMA;
+      dma_load16(make_rsrc_sgpr(KN ? Bbase + (int64_t)k0 * ldb : Bbase + k0), b_kx[i] < krem ? b_off[i] : kBufOOB,
+                 sA + S::A_BYTES + (wave * S::B_DMA + i) * 1024);
+    }
+  };
+
+  // ---- fragment addresses: lane (r16 = lane%16, G = lane/16) supplies row/column r16
+  // and k = 8G .. 8G+7 of a 32-k sub-step ----
+  const int r16 = lane & 15, G = lane >> 4;
+  uint32_t fa_off[2];  // A block 0 of sub-step s (block i: + 16 rows = 2048 bytes)
+#pragma unroll
+  for (int s = 0; s < 2; ++s) fa_off[s] = lds_off128(wm * S::WTM + r16, 4 * s + G);
+  uint32_t fb_off[KN ? FN : 2];
+  if (KN) {
+    // lanes of group G point at k row 8G + r16/4 (+4 for the second read, +32 for sub-step
+    // 1), columns 16j + 4(r16%4) of the wave's block: a transposing read hands lane r16 of
+    // the group column 16j + r16 at four consecutive k
+    const int kr = 8 * G + (r16 >> 2);
+#pragma unroll
+    for (int j = 0; j < (KN ? FN : 2); ++j) {
+      const int cb = (wn * S::WTN + 16 * j + 4 * (r16 & 3)) * 2;  // byte column
+      fb_off[j] = (uint32_t)(kr * S::B_PITCH + (((cb >> 6) ^ (kr & 3)) << 6) + (cb & 63));
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) fb_off[s] = lds_off128(wn * S::WTN + r16, 4 * s + G);
+  }
+
+  f32x4 acc[FM][FN];
+  static_for<FM * FN>([&](auto xc) {
+    constexpr int x = decltype(xc)::value;
+    acc[x / FN][x % FN] = f32x4{0.f, 0.f, 0.f, 0.f};
+  });
+
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  u32x4 fa[2][FM], fb[2][FN];
+  // LDS read r of sub-step s of step kt into fragment buffer buf: r < FM reads A block r;
+  // then B (two transposing reads per block for [K,N], one ds_read_b128 for [N,K]).
+  constexpr int RD = FM + (KN ? 2 : 1) * FN;
+  auto read_one = [&](int kt, int s, int buf, auto rc) {
+    constexpr int r = decltype(rc)::value;
+    const unsigned char* st = smem + (kt & 1) * S::STAGE;
+    if constexpr (r < FM) {
+      fa[buf][r] = *(const u32x4*)(st + fa_off[s] + r * 16 * S::ROW);
+    } else if constexpr (KN) {
+      constexpr int j = (r - FM) >> 1, half = (r - FM) & 1;
+      const unsigned char* q = st + S::A_BYTES + fb_off[j] + (32 * s + 4 * half) * S::B_PITCH;
+      const u32x2 v = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q));
+      if constexpr (half == 0) {
+        fb[buf][j].x = v.x;
+        fb[buf][j].y = v.y;
+      } else {
+        fb[buf][j].z = v.x;
+        fb[buf][j].w = v.y;
+      }
+    } else {
+      constexpr int j = r - FM;
+      fb[buf][j] = *(const u32x4*)(st + S::A_BYTES + fb_off[s] + j * 16 * S::ROW);
+    }
+  };
+  // One 32-k sub-step of MFMAs on fragment buffer BUF; slot x also issues read
+  // r * X / RD == x of sub-step (rkt, rs) into the other buffer and, when WITH_DMA,
+  // DMA piece d * X / DMA == x of step dkt.
+  constexpr int X = FM * FN;
+  auto substep = [&](auto bufc, int rkt, int rs, auto dmac, int dkt) {
+    constexpr int buf = decltype(bufc)::value;
+    constexpr bool with_dma = decltype(dmac)::value;
+    static_for<X>([&](auto xc) {
+      constexpr int x = decltype(xc)::value;
+      constexpr int i = x / FN, j = x % FN;
+      acc[i][j] = Mfma<T>::mma(fb[buf][j], fa[buf][i], acc[i][j]);
+      static_for<RD>([&](auto rc) {
+        if constexpr (decltype(rc)::value * X / RD == x) read_one(rkt, rs, buf ^ 1, rc);
+      });
+      if constexpr (with_dma) {
+        static_for<S::DMA>([&](auto dc) {
+          constexpr int d = decltype(dc)::value;
+          if constexpr (d * X / S::DMA == x) dma_piece(dkt, d);
+        });
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the slots in this order
+    });
+  };
+
+  const int nk = (K + S::BK - 1) / S::BK;
+  if (nk > 0) {
+#pragma unroll
+    for (int d = 0; d < S::DMA; ++d) dma_piece(0, d);
+#pragma unroll
+    for (int d = 0; d < S::DMA; ++d) dma_piece(1, d);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(S::DMA) : "memory");  // step 0 landed
+    static_for<RD>([&](auto rc) { read_one(0, 0, 0, rc); });
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    for (int kt = 0; kt < nk; ++kt) {
+      substep(B0{}, kt, 1, std::false_type{}, 0);
+      // every read of slot kt done and step kt+1 landed (this wave), then barrier
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" : : : "memory");
+      substep(B1{}, kt + 1, 0, std::true_type{}, kt + 2);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // no LDS DMA may outlive the workgroup
+  }
+
+  // ---- epilogue: acc[i][j][e] = C[m = 16i + r16][n = 16j + 4G + e] of the wave's block.
+  // For a pair of blocks (j, j+1), one v_permlane16_swap per dword trades G = 1's columns
+  // of block j for G = 0's of block j+1 (and G = 3's of j for G = 2's of j+1): lane (r16, G)
+  // then holds columns 16j' + 8(G/2) .. +7 of block j' = j + G%2. ----
+  T* Cb = (T*)p.C + bz * p.stride_c;
+  const uint16_t* bias = (const uint16_t*)p.bias;
+  const bool st16 = (p.ldc & 7) == 0;
+  const int mw = m0 + wm * S::WTM, nw = n0 + wn * S::WTN;
+  auto bias_add = [&](int i, int j, f32x4 v) {
+    if constexpr (BIAS == 2) {
+      const int m = mw + 16 * i + r16;
+      const float b = m < M ? from_bits<T>(bias[m]) : 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += b;
+    } else if constexpr (BIAS == 1) {
+      // four consecutive bias values: one 8-byte load when all four exist, else one
+      // 2-byte load each (a descriptor of 2N bytes returns zeros past N)
+      const int n = nw + 16 * j + 4 * G;
+      const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(bias), 0, 2 * N, kBufWord3);
+      u32x2 bb;
+      if (n + 4 <= N) {
+        bb = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(br, (uint32_t)(2 * n), 0, 0));
+      } else {
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = buf_load2(br, (uint32_t)(2 * (n + e)));
+        bb = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+      }
+      v[0] += from_bits<T>((uint16_t)(bb.x & 0xFFFF));
+      v[1] += from_bits<T>((uint16_t)(bb.x >> 16));
+      v[2] += from_bits<T>((uint16_t)(bb.y & 0xFFFF));
+      v[3] += from_bits<T>((uint16_t)(bb.y >> 16));
+    }
+    return v;
+  };
+  static_for<FM>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    const int m = mw + 16 * i + r16;
+    static_for<(FN + 1) / 2>([&](auto qc) {
+      constexpr int j = 2 * decltype(qc)::value;
+      const f32x4 v0 = bias_add(i, j, acc[i][j]);
+      uint32_t P0[2] = {pack2<T>(v0[0], v0[1]), pack2<T>(v0[2], v0[3])};
+      if constexpr (j + 1 < FN) {
+        const f32x4 v1 = bias_add(i, j + 1, acc[i][j + 1]);
+        uint32_t P1[2] = {pack2<T>(v1[0], v1[1]), pack2<T>(v1[2], v1[3])};
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          const auto sw = __builtin_amdgcn_permlane16_swap(P0[w], P1[w], false, false);
+          P0[w] = sw[0];
+          P1[w] = sw[1];
+        }
+        const int n = nw + 16 * (j + (G & 1)) + 8 * (G >> 1);
+        if (m < M && n < N) {
+          T* dst = Cb + (int64_t)m * p.ldc + n;
+          const u32x4 v = {P0[0], P0[1], P1[0], P1[1]};
+          if (n + 8 <= N && st16) {
+            *(u32x4*)dst = v;
+          } else if (n + 8 <= N) {  // ldc % 8 == 4: 8-byte aligned rows
+            *(u32x2*)dst = u32x2{v.x, v.y};
+            *(u32x2*)(dst + 4) = u32x2{v.z, v.w};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (n + e < N) ((uint16_t*)dst)[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+          }
+        }
+      } else {  // odd last block: four columns per lane
+        const int n = nw + 16 * j + 4 * G;
+        if (m < M && n < N) {
+          T* dst = Cb + (int64_t)m * p.ldc + n;
+          const u32x2 v = {P0[0], P0[1]};
+          if (n + 4 <= N) {
+            *(u32x2*)dst = v;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < N) ((uint16_t*)dst)[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+          }
+        }
+      }
+    });
+  });
+}
+
+// Launches gemm_tile16_kernel with the bias mode the arguments ask for.
+template <typename T, bool KN, int BM, int BN>
+void launch_tile16(const GemmParams& p, dim3 grid, hipStream_t s) {
+  if (p.bias == nullptr)
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 0>), grid, dim3(256), 0, s, p);
+  else if (p.bias_row)
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 2>), grid, dim3(256), 0, s, p);
+  else
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 1>), grid, dim3(256), 0, s, p);
+}
+
+}  // namespace cmpext3

@@ -1,5 +1,6 @@
 // Instantiations of the tiled MFMA GEMM for fp16.
 #include "kernels.h"
+#include "tile16_kernel.h"
 #include "tile_kernel.h"
 
 namespace cmpext3 {
@@ -8,10 +9,10 @@ template <bool KN>
 hipError_t launch(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s) {
   switch (id) {
     case kTile256x256:
-      hipLaunchKernelGGL((gemm_tile_kernel<_Float16, KN, 256, 256, 2, 2, 2, 64>), grid, dim3(256), 0, s, p);
+      launch_tile16<_Float16, KN, 256, 256>(p, grid, s);
       break;
     case kTile256x224:
-      hipLaunchKernelGGL((gemm_tile_kernel<_Float16, KN, 256, 224, 4, 1, 2, 64>), grid, dim3(256), 0, s, p);
+      launch_tile16<_Float16, KN, 256, 224>(p, grid, s);
       break;
     case kTile128x128:
       hipLaunchKernelGGL((gemm_tile_kernel<_Float16, KN, 128, 128, 2, 2, 5>), grid, dim3(256), 0, s, p);

@@ -190,7 +190,8 @@ def test_fp16_overflow_matches_rounding():
 
 # ------------------------------------------------------- layouts, views, bias
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
-@pytest.mark.parametrize("shape", [(2, 150, 72, 200), (1, 4096, 4096, 4096), (3, 7, 40, 12), (1, 16, 64, 64)])
+@pytest.mark.parametrize("shape", [(2, 150, 72, 200), (1, 4096, 4096, 4096), (3, 7, 40, 12), (1, 16, 64, 64),
+                                   (1, 2048, 512, 1004), (1, 4096, 512, 3588), (2, 2048, 1024, 3588)])
 def test_linear_with_bias(dtype, shape):
     Bt, S, K, N = shape
     g = torch.Generator().manual_seed(sum(shape))
