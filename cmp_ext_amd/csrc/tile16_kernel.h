@@ -78,8 +78,8 @@ struct Tile16Shape {
 // BIAS: 0 none, 1 per column of C (Linear), 2 per row (conv 1x1).  A kernel per
 // mode keeps the bias-free epilogue lean: the register allocator then keeps the
 // accumulators in AGPRs through the main loop.
-template <typename T, bool KN, int BM, int BN, int BIAS>
-__global__ void __launch_bounds__(256, 1) gemm_tile16_kernel(const GemmParams p) {
+template <typename T, bool KN, int BM, int BN, int BIAS, int MINB = 1>
+__global__ void __launch_bounds__(256, MINB) gemm_tile16_kernel(const GemmParams p) {
   using S = Tile16Shape<BM, BN, KN>;
   constexpr int FM = S::FM, FN = S::FN;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[S::LDS];
@@ -321,15 +321,16 @@ __global__ void __launch_bounds__(256, 1) gemm_tile16_kernel(const GemmParams p)
   });
 }
 
-// Launches gemm_tile16_kernel with the bias mode the arguments ask for.
-template <typename T, bool KN, int BM, int BN>
+// Launches gemm_tile16_kernel with the bias mode the arguments ask for; MINB
+// workgroups per CU is the occupancy the kernel is compiled for.
+template <typename T, bool KN, int BM, int BN, int MINB = 1>
 void launch_tile16(const GemmParams& p, dim3 grid, hipStream_t s) {
   if (p.bias == nullptr)
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 0>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 0, MINB>), grid, dim3(256), 0, s, p);
   else if (p.bias_row)
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 2>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 2, MINB>), grid, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 1>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 1, MINB>), grid, dim3(256), 0, s, p);
 }
 
 }  // namespace cmpext3
