@@ -140,6 +140,7 @@ int make_plan(const Request& r, Plan* plan) {
       p.kernel = c->id;
       p.bm = c->bm;
       p.bn = c->bn;
+      if (c->id != kTile128x128) p.threads = 512;  // the 256-row tiles run 8 waves
     } else {
       p.kernel = kGeneric16;
       p.bm = 64;

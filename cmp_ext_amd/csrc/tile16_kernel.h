@@ -6,13 +6,15 @@
 // A[M,K], B[K,N], C[M,N]; zero-filled out-of-range loads, per-element masked
 // stores), built around the CDNA4 matrix cores and accumulating in fp32.
 //
-// Structure (one workgroup of 4 waves in a 2 x 2 grid = one BM x BN tile):
-//   * Each wave owns a (BM/2) x (BN/2) block of C as (BM/32) x (BN/32) blocks of
-//     16 x 16 fp32 accumulators (AGPRs), fed by v_mfma_f32_16x16x32_{f16,bf16}.
-//     A 16-wide block grain lets a 256 x 224 tile (the MLP shape) keep the
-//     2 x 2 wave grid; the 2 x 2 grid reads the fewest fragment bytes from LDS
-//     per MFMA.  Measured on MI355X, this kernel also holds a higher shader
-//     clock under the power limit than the same tile on 32x32x16 products.
+// Structure (one workgroup of 8 waves in a 4 x 2 grid = one BM x BN tile):
+//   * Each wave owns a (BM/4) x (BN/2) block of C as (BM/64) x (BN/32) blocks of
+//     16 x 16 fp32 accumulators, fed by v_mfma_f32_16x16x32_{f16,bf16}.  A
+//     16-wide block grain lets a 256 x 224 tile (the MLP shape) use the same
+//     grid.  Eight waves put two on each SIMD (at most 256 VGPRs each), so one
+//     wave's matrix products run while the other waits on LDS reads or on the
+//     issue of its LDS-DMA loads; measured on MI355X this beats four waves of
+//     twice the block (fewer fragment bytes per MFMA, but one wave per SIMD)
+//     by ~9 % in loop cycles and halves the epilogue.
 //   * K steps of BK = 64 go global -> LDS by buffer_load_dwordx4 ... lds (LDS
 //     DMA: no registers, no ds_write) into a two-stage ring.  A step is two
 //     sub-steps of 32 k.  All reads of a step's slot are issued by the end of its
@@ -55,22 +57,27 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
+// 8 waves in a 4 x 2 grid: two waves per SIMD, so one wave's MFMAs cover the other's
+// LDS waits and DMA issue.
+constexpr int kT16WavesM = 4, kT16WavesN = 2, kT16Threads = 64 * kT16WavesM * kT16WavesN;
+
 template <int BM, int BN, bool KN>
 struct Tile16Shape {
   static constexpr int BK = 64;
   static constexpr int ROW = BK * 2;  // bytes per LDS row of a K-contiguous operand
-  static constexpr int WTM = BM / 2, WTN = BN / 2;
+  static constexpr int NW = kT16WavesM * kT16WavesN;
+  static constexpr int WTM = BM / kT16WavesM, WTN = BN / kT16WavesN;
   static constexpr int FM = WTM / 16, FN = WTN / 16;
   static constexpr int A_BYTES = BM * ROW;
   static constexpr int B_PITCH = KN ? (BN * 2 + 255) / 256 * 256 : ROW;  // bytes per LDS row of B
   static constexpr int B_BYTES = KN ? BK * B_PITCH : (BN + 63) / 64 * 64 * ROW;  // rows >= BN are OOB
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int LDS = 2 * STAGE;
-  static constexpr int A_DMA = A_BYTES / 1024 / 4;  // 1 KB LDS-DMA loads per wave per step
-  static constexpr int B_DMA = B_BYTES / 1024 / 4;
+  static constexpr int A_DMA = A_BYTES / 1024 / NW;  // 1 KB LDS-DMA loads per wave per step
+  static constexpr int B_DMA = B_BYTES / 1024 / NW;
   static constexpr int DMA = A_DMA + B_DMA;
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "16-row/column blocks");
-  static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "whole DMA loads per wave");
+  static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "whole DMA loads per wave");
   static_assert(LDS <= 160 * 1024, "LDS budget");
   static_assert(DMA <= 63, "vmcnt range");
 };
@@ -79,7 +86,7 @@ struct Tile16Shape {
 // mode keeps the bias-free epilogue lean: the register allocator then keeps the
 // accumulators in AGPRs through the main loop.
 template <typename T, bool KN, int BM, int BN, int BIAS, int MINB = 1>
-__global__ void __launch_bounds__(256, MINB) gemm_tile16_kernel(const GemmParams p) {
+__global__ void __launch_bounds__(kT16Threads, MINB) gemm_tile16_kernel(const GemmParams p) {
   using S = Tile16Shape<BM, BN, KN>;
   constexpr int FM = S::FM, FN = S::FN;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[S::LDS];
@@ -87,7 +94,7 @@ __global__ void __launch_bounds__(256, MINB) gemm_tile16_kernel(const GemmParams
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / kT16WavesN, wn = wave % kT16WavesN;
 
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
@@ -326,11 +333,11 @@ __global__ void __launch_bounds__(256, MINB) gemm_tile16_kernel(const GemmParams
 template <typename T, bool KN, int BM, int BN, int MINB = 1>
 void launch_tile16(const GemmParams& p, dim3 grid, hipStream_t s) {
   if (p.bias == nullptr)
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 0, MINB>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 0, MINB>), grid, dim3(kT16Threads), 0, s, p);
   else if (p.bias_row)
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 2, MINB>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 2, MINB>), grid, dim3(kT16Threads), 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 1, MINB>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 1, MINB>), grid, dim3(kT16Threads), 0, s, p);
 }
 
 }  // namespace cmpext3
