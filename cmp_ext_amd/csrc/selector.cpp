@@ -19,17 +19,18 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 struct Candidate {
   KernelId id;
   int bm, bn;
-  double eff;  // relative per-flop throughput of a CU running this tile (measured)
+  int occ;     // workgroups a CU runs at once (1 unless the kernel is built for more)
+  double eff;  // relative per-flop throughput of a CU running occ of these tiles (measured)
 };
 
-// Modelled cost of running the tiles of bm x bn: the busiest CU gets
-// ceil(tiles / kNumCUs) of them (workgroups are handed out as slots free, and
-// a CU's matrix cores are shared by whatever it holds), each worth
-// bm * bn / eff.  Measured on MI355X this tracks the time of the fp32 and
+// Modelled cost of running the tiles of bm x bn: tiles go out in rounds of
+// kNumCUs * occ (workgroups are handed out as slots free, and a CU's matrix
+// cores are shared by whatever it holds); a round is worth occ * bm * bn / eff
+// on the busiest CU.  Measured on MI355X this tracks the time of the fp32 and
 // 16-bit tile kernels across 512^3 .. 4096^3 and ragged shapes.
 double tile_cost(const Candidate& c, int64_t M, int64_t N, int64_t batch) {
   const int64_t tiles = cdiv(M, c.bm) * cdiv(N, c.bn) * batch;
-  return (double)cdiv(tiles, kNumCUs) * c.bm * c.bn / c.eff;
+  return (double)cdiv(tiles, (int64_t)kNumCUs * c.occ) * c.occ * c.bm * c.bn / c.eff;
 }
 
 const Candidate* pick(const Candidate* c, int n, int64_t M, int64_t N, int64_t batch) {
@@ -45,18 +46,18 @@ const Candidate* pick(const Candidate* c, int n, int64_t M, int64_t N, int64_t b
   return best;
 }
 
-// Per-area throughput of a CU running the tile, relative to 256x256 (MI355X: one
-// round of 256x256 tiles at K = 2048 takes ~54 us, one of 128x128 tiles ~27 us).
+// Per-area throughput of a CU running the tile, relative to 256x256 (MI355X, fp16
+// 4096^3: 256x256 102.7 us, 128x128 with two workgroups per CU 126.7 us).
 const Candidate kTiles16[] = {
-    {kTile256x256, 256, 256, 1.00},
-    {kTile256x224, 256, 224, 0.98},
-    {kTile128x128, 128, 128, 0.50},
+    {kTile256x256, 256, 256, 1, 1.00},
+    {kTile256x224, 256, 224, 1, 0.98},
+    {kTile128x128, 128, 128, 2, 0.81},
 };
 // fp32 4096^3 on MI355X: 128x128 126 TFLOP/s, 96x64 115, 64x64 115.
 const Candidate kTiles32[] = {
-    {kF32Tile128, 128, 128, 1.00},
-    {kF32Tile96x64, 96, 64, 0.915},
-    {kF32Tile64, 64, 64, 0.91},
+    {kF32Tile128, 128, 128, 1, 1.00},
+    {kF32Tile96x64, 96, 64, 1, 0.915},
+    {kF32Tile64, 64, 64, 1, 0.91},
 };
 
 const char* kernel_name(KernelId id) {
@@ -140,7 +141,7 @@ int make_plan(const Request& r, Plan* plan) {
       p.kernel = c->id;
       p.bm = c->bm;
       p.bn = c->bn;
-      if (c->id != kTile128x128) p.threads = 512;  // the 256-row tiles run 8 waves
+      if (c->id != kTile128x128) p.threads = 512;  // the 256-row tiles run 8 waves, 128x128 4
     } else {
       p.kernel = kGeneric16;
       p.bm = 64;

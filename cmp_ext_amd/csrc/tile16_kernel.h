@@ -6,15 +6,16 @@
 // A[M,K], B[K,N], C[M,N]; zero-filled out-of-range loads, per-element masked
 // stores), built around the CDNA4 matrix cores and accumulating in fp32.
 //
-// Structure (one workgroup of 8 waves in a 4 x 2 grid = one BM x BN tile):
-//   * Each wave owns a (BM/4) x (BN/2) block of C as (BM/64) x (BN/32) blocks of
-//     16 x 16 fp32 accumulators, fed by v_mfma_f32_16x16x32_{f16,bf16}.  A
-//     16-wide block grain lets a 256 x 224 tile (the MLP shape) use the same
-//     grid.  Eight waves put two on each SIMD (at most 256 VGPRs each), so one
-//     wave's matrix products run while the other waits on LDS reads or on the
-//     issue of its LDS-DMA loads; measured on MI355X this beats four waves of
-//     twice the block (fewer fragment bytes per MFMA, but one wave per SIMD)
-//     by ~9 % in loop cycles and halves the epilogue.
+// Structure (one workgroup of WM x WN waves = one BM x BN tile):
+//   * Each wave owns a (BM/WM) x (BN/WN) block of C as 16 x 16 blocks of fp32
+//     accumulators, fed by v_mfma_f32_16x16x32_{f16,bf16}.  The 16-wide block
+//     grain lets a 256 x 224 tile (the MLP shape) use the same grid as 256 x 256.
+//   * Two waves per SIMD: the 256-row tiles run 8 waves (4 x 2, at most 256
+//     VGPRs each) in one workgroup per CU, the 128 x 128 tile 4 waves (2 x 2) in
+//     two workgroups per CU.  One wave's matrix products then run while the other
+//     waits on LDS reads or on the issue of its LDS-DMA loads; measured on
+//     MI355X, 8 waves beat 4 waves of twice the block (fewer fragment bytes per
+//     MFMA, one wave per SIMD) by ~9 % in loop cycles and halve the epilogue.
 //   * K steps of BK = 64 go global -> LDS by buffer_load_dwordx4 ... lds (LDS
 //     DMA: no registers, no ds_write) into a two-stage ring.  A step is two
 //     sub-steps of 32 k.  All reads of a step's slot are issued by the end of its
@@ -42,7 +43,6 @@
 #include <utility>
 
 #include "device_common.h"
-#include "tile_kernel.h"  // lds_off128, dma_kn_geom
 
 namespace cmpext3 {
 
@@ -57,16 +57,24 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// 8 waves in a 4 x 2 grid: two waves per SIMD, so one wave's MFMAs cover the other's
-// LDS waits and DMA issue.
-constexpr int kT16WavesM = 4, kT16WavesN = 2, kT16Threads = 64 * kT16WavesM * kT16WavesN;
+// [k][n] layout of an N-contiguous B tile: rows of `pitch` bytes (a multiple
+// of 256), 64-byte segments XORed with k%4.  Lane `lane` of 1 KB LDS-DMA load
+// `slot` fetches row k, columns n..n+7 (the inverse of the layout at byte
+// slot*1024 + 16*lane).
+__device__ __forceinline__ void dma_kn_geom(int slot, int lane, int pitch, int& k, int& n) {
+  const int pos = slot * 1024 + 16 * lane;
+  k = pos / pitch;
+  const int within = pos - k * pitch;
+  const int seg = (within >> 6) ^ (k & 3);
+  n = (seg * 64 + (within & 63)) >> 1;
+}
 
-template <int BM, int BN, bool KN>
+template <int BM, int BN, bool KN, int WM, int WN>
 struct Tile16Shape {
   static constexpr int BK = 64;
   static constexpr int ROW = BK * 2;  // bytes per LDS row of a K-contiguous operand
-  static constexpr int NW = kT16WavesM * kT16WavesN;
-  static constexpr int WTM = BM / kT16WavesM, WTN = BN / kT16WavesN;
+  static constexpr int NW = WM * WN;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int FM = WTM / 16, FN = WTN / 16;
   static constexpr int A_BYTES = BM * ROW;
   static constexpr int B_PITCH = KN ? (BN * 2 + 255) / 256 * 256 : ROW;  // bytes per LDS row of B
@@ -85,16 +93,16 @@ struct Tile16Shape {
 // BIAS: 0 none, 1 per column of C (Linear), 2 per row (conv 1x1).  A kernel per
 // mode keeps the bias-free epilogue lean: the register allocator then keeps the
 // accumulators in AGPRs through the main loop.
-template <typename T, bool KN, int BM, int BN, int BIAS, int MINB = 1>
-__global__ void __launch_bounds__(kT16Threads, MINB) gemm_tile16_kernel(const GemmParams p) {
-  using S = Tile16Shape<BM, BN, KN>;
+template <typename T, bool KN, int BM, int BN, int WM, int WN, int BIAS, int MINB>
+__global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const GemmParams p) {
+  using S = Tile16Shape<BM, BN, KN, WM, WN>;
   constexpr int FM = S::FM, FN = S::FN;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[S::LDS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  const int wm = wave / kT16WavesN, wn = wave % kT16WavesN;
+  const int wm = wave / WN, wn = wave % WN;
 
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
@@ -328,16 +336,17 @@ __global__ void __launch_bounds__(kT16Threads, MINB) gemm_tile16_kernel(const Ge
   });
 }
 
-// Launches gemm_tile16_kernel with the bias mode the arguments ask for; MINB
-// workgroups per CU is the occupancy the kernel is compiled for.
-template <typename T, bool KN, int BM, int BN, int MINB = 1>
+// Launches gemm_tile16_kernel (WM x WN waves, MINB workgroups per CU) with the
+// bias mode the arguments ask for.
+template <typename T, bool KN, int BM, int BN, int WM, int WN, int MINB>
 void launch_tile16(const GemmParams& p, dim3 grid, hipStream_t s) {
+  const dim3 block(64 * WM * WN);
   if (p.bias == nullptr)
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 0, MINB>), grid, dim3(kT16Threads), 0, s, p);
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 0, MINB>), grid, block, 0, s, p);
   else if (p.bias_row)
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 2, MINB>), grid, dim3(kT16Threads), 0, s, p);
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 2, MINB>), grid, block, 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, 1, MINB>), grid, dim3(kT16Threads), 0, s, p);
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 1, MINB>), grid, block, 0, s, p);
 }
 
 }  // namespace cmpext3
