@@ -8,13 +8,13 @@ template <bool KN>
 hipError_t launch(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s) {
   switch (id) {
     case kF32Tile128:
-      hipLaunchKernelGGL((gemm_f32_kernel<KN, 128, 128, 2>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((gemm_f32_kernel<KN, 128, 128, 2, 4>), grid, dim3(256), 0, s, p);
       break;
     case kF32Tile96x64:
-      hipLaunchKernelGGL((gemm_f32_kernel<KN, 96, 64, 2>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((gemm_f32_kernel<KN, 96, 64, 2, 8>), grid, dim3(256), 0, s, p);
       break;
     case kF32Tile64:
-      hipLaunchKernelGGL((gemm_f32_kernel<KN, 64, 64, 2>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((gemm_f32_kernel<KN, 64, 64, 2, 8>), grid, dim3(256), 0, s, p);
       break;
     default:
       return hipErrorInvalidValue;
