@@ -27,7 +27,7 @@
 //   * A (and B given as [N,K]) are K-contiguous: LDS rows of 128 bytes in the
 //     lds_off128 layout, one ds_read_b128 per 16 x 32 fragment, conflict free.
 //   * B given as [K,N] stays [k][n] in LDS (rows padded to a multiple of 256
-//     bytes, 64-byte segments XORed with k%4) and is read with
+//     bytes, swizzled by kn_off) and is read with
 //     ds_read_b64_tr_b16, the CDNA4 transposing LDS read: two per fragment.
 //   * Out-of-range pieces (rows >= M, columns >= N, k >= K) use an offset past
 //     the buffer descriptor's range: the hardware writes zeros into LDS.
@@ -58,15 +58,22 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // [k][n] layout of an N-contiguous B tile: rows of `pitch` bytes (a multiple
-// of 256), 64-byte segments XORed with k%4.  Lane `lane` of 1 KB LDS-DMA load
-// `slot` fetches row k, columns n..n+7 (the inverse of the layout at byte
-// slot*1024 + 16*lane).
+// of 256), 64-byte segments XORed with k%4 and their 32-byte halves with
+// (k/8)%2.  A transposing fragment read (lanes of group G at rows 8G + 0..3,
+// 8 bytes each) then covers all 64 banks once per 32 lanes; without the half
+// swap, groups G and G+1 hit the same 32 banks (measured: 8.5M bank-conflict
+// cycles per 4096^3 launch, now 0).
+__device__ __forceinline__ uint32_t kn_off(int k, int pitch, int byte_col) {
+  return (uint32_t)(k * pitch + (((byte_col >> 6) ^ (k & 3)) << 6) + ((byte_col & 63) ^ (((k >> 3) & 1) << 5)));
+}
+// Lane `lane` of 1 KB LDS-DMA load `slot` fetches row k, columns n..n+7 (the
+// inverse of kn_off at byte slot*1024 + 16*lane).
 __device__ __forceinline__ void dma_kn_geom(int slot, int lane, int pitch, int& k, int& n) {
   const int pos = slot * 1024 + 16 * lane;
   k = pos / pitch;
   const int within = pos - k * pitch;
   const int seg = (within >> 6) ^ (k & 3);
-  n = (seg * 64 + (within & 63)) >> 1;
+  n = (seg * 64 + ((within & 63) ^ (((k >> 3) & 1) << 5))) >> 1;
 }
 
 template <int BM, int BN, bool KN, int WM, int WN>
@@ -169,7 +176,7 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
 #pragma unroll
     for (int j = 0; j < (KN ? FN : 2); ++j) {
       const int cb = (wn * S::WTN + 16 * j + 4 * (r16 & 3)) * 2;  // byte column
-      fb_off[j] = (uint32_t)(kr * S::B_PITCH + (((cb >> 6) ^ (kr & 3)) << 6) + (cb & 63));
+      fb_off[j] = kn_off(kr, S::B_PITCH, cb);  // + (32s + 4 half) rows keeps both swizzle terms
     }
   } else {
 #pragma unroll
