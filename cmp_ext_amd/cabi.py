@@ -24,6 +24,9 @@ SIGNATURES = {
     "cmpext3_matmul_fp16": (_i, [_p, _p, _p, _i, _i, _i, _p]),
     "cmpext3_matmul_bf16": (_i, [_p, _p, _p, _i, _i, _i, _p]),
     "cmpext3_matmul_fp32": (_i, [_p, _p, _p, _i, _i, _i, _p]),
+    "cmpext3_gemm_f16": (_i, [_p, _i64, _p, _i64, _p, _i64, _i, _i, _i, _p]),
+    "cmpext3_gemm_bf16": (_i, [_p, _i64, _p, _i64, _p, _i64, _i, _i, _i, _p]),
+    "cmpext3_gemm_f32": (_i, [_p, _i64, _p, _i64, _p, _i64, _i, _i, _i, _p]),
     "cmpext3_gemm_ex": (_i, [_i, _i, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p,
                              _i, _i, _i, _i, _p, _i64, _p]),
     "cmpext3_conv2d_1x1": (_i, [_i, _p, _p, _p, _p, _i, _i, _i, _i, _p, _i64, _p]),
@@ -101,6 +104,12 @@ def conv2d_1x1(dtype: int, inp, weight, bias, out, batch: int, c_in: int, c_out:
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     return lib().cmpext3_conv2d_1x1(dtype, ptr(inp), ptr(weight), ptr(bias), ptr(out), batch, c_in, c_out,
                                     hw, ptr(workspace), ws_bytes, _stream_handle(stream))
+
+
+def gemm_strided(dtype: int, A, lda: int, B, ldb: int, C, ldc: int, M: int, N: int, K: int, stream=None) -> int:
+    """Call cmpext3_gemm_{f16,bf16,f32} (row pitches in elements; A, B, C may be views)."""
+    fn = {F16: lib().cmpext3_gemm_f16, BF16: lib().cmpext3_gemm_bf16, F32: lib().cmpext3_gemm_f32}[dtype]
+    return fn(A.data_ptr(), lda, B.data_ptr(), ldb, C.data_ptr(), ldc, M, N, K, _stream_handle(stream))
 
 
 def matmul(dtype: int, A, B, C, M: int, N: int, K: int, stream=None) -> int:

@@ -146,6 +146,24 @@ extern "C" int cmpext3_matmul_fp32(const float* A, const float* B, float* C, int
                          nullptr, M, N, K, 1, nullptr, 0, stream);
 }
 
+extern "C" int cmpext3_gemm_f16(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
+                                int M, int N, int K, void* stream) {
+  return cmpext3_gemm_ex(CMPEXT3_F16, CMPEXT3_B_KN, A, lda, 0, B, ldb, 0, C, ldc, 0, nullptr, M, N, K, 1, nullptr,
+                         0, stream);
+}
+
+extern "C" int cmpext3_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
+                                 int M, int N, int K, void* stream) {
+  return cmpext3_gemm_ex(CMPEXT3_BF16, CMPEXT3_B_KN, A, lda, 0, B, ldb, 0, C, ldc, 0, nullptr, M, N, K, 1, nullptr,
+                         0, stream);
+}
+
+extern "C" int cmpext3_gemm_f32(const float* A, int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc,
+                                int M, int N, int K, void* stream) {
+  return cmpext3_gemm_ex(CMPEXT3_F32, CMPEXT3_B_KN, A, lda, 0, B, ldb, 0, C, ldc, 0, nullptr, M, N, K, 1, nullptr,
+                         0, stream);
+}
+
 namespace {
 Request plan_request(int dtype, int b_layout, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc, int align,
                      int has_bias, int batch, int64_t ws_bytes) {

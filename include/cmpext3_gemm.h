@@ -62,6 +62,23 @@ int cmpext3_matmul_bf16(const void* A, const void* B, void* C, int M, int N, int
 int cmpext3_matmul_fp32(const float* A, const float* B, float* C, int M, int N, int K, void* stream);
 
 /*
+ * Strided row-major forms: C[M,N] = A[M,K] * B[K,N] with row pitches lda >= K,
+ * ldb >= N, ldc >= N (elements), fp32 accumulation, output in the input dtype
+ * (fp32 MFMA for _f32).  The launchers above with explicit pitches, so a caller
+ * holding row-pitched views (e.g. a column slice of a larger matrix) needs no
+ * copy.  No workspace: M <= 64 products take the unsplit skinny kernel.
+ * Replace launch_matmul_fp16/bf16/fp32 (src/cuda/fp16_matmul.cu:301-340,
+ * bf16_matmul.cu:232-254, fp32_matmul.cu:236-265), which fix lda=K, ldb=N,
+ * ldc=N (fp16_matmul.cu:311-313).
+ */
+int cmpext3_gemm_f16(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
+                     int M, int N, int K, void* stream);
+int cmpext3_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
+                      int M, int N, int K, void* stream);
+int cmpext3_gemm_f32(const float* A, int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc,
+                     int M, int N, int K, void* stream);
+
+/*
  * General form used by the Python bindings for matmul, linear and bmm:
  *   for b in [0, batch):  C_b = A_b * op(B_b) (+ bias)
  * with A_b = A + b*stride_a (elements), etc.; op(B) = B for CMPEXT3_B_KN and

@@ -20,7 +20,8 @@ def declared_symbols():
 
 def test_header_declares_expected_entry_points():
     syms = declared_symbols()
-    for s in ["cmpext3_matmul_fp16", "cmpext3_matmul_bf16", "cmpext3_matmul_fp32", "cmpext3_gemm_ex",
+    for s in ["cmpext3_matmul_fp16", "cmpext3_matmul_bf16", "cmpext3_matmul_fp32", "cmpext3_gemm_f16",
+              "cmpext3_gemm_bf16", "cmpext3_gemm_f32", "cmpext3_gemm_ex",
               "cmpext3_gemm_workspace_size", "cmpext3_gemm_plan", "cmpext3_status_string", "cmpext3_version"]:
         assert s in syms
 
@@ -69,6 +70,7 @@ def test_empty_problems_launch_nothing():
     assert lib.cmpext3_gemm_ex(cabi.BF16, cabi.B_NK, None, 8, 0, None, 8, 0, None, 8, 0, None, 8, 8, 8, 0, None, 0,
                                None) == 0
     assert lib.cmpext3_matmul_fp16(None, None, None, 0, 0, 0, None) == 0
+    assert lib.cmpext3_gemm_bf16(None, 8, None, 8, None, 8, 8, 0, 8, None) == 0
     # skinny-M shapes with no columns or no batch entries (the split-K planner divides by both)
     assert lib.cmpext3_gemm_ex(cabi.F16, cabi.B_KN, None, 8, 0, None, 8, 0, None, 8, 0, None, 8, 0, 8, 1, None, 0,
                                None) == 0
@@ -76,6 +78,15 @@ def test_empty_problems_launch_nothing():
                                None) == 0
     assert cabi.workspace_size(cabi.F16, cabi.B_KN, 16, 0, 8192) == 0
     assert cabi.workspace_size(cabi.BF16, cabi.B_KN, 16, 8192, 8192, batch=0) == 0
+
+
+def test_strided_entry_points_check_pitches():
+    lib = cabi.lib()
+    # pitches below the row length are rejected before any launch
+    assert lib.cmpext3_gemm_f16(0x1000, 63, 0x2000, 64, 0x3000, 64, 64, 64, 64, None) == cabi.ERR_INVALID_ARG
+    assert lib.cmpext3_gemm_bf16(0x1000, 64, 0x2000, 32, 0x3000, 64, 64, 64, 64, None) == cabi.ERR_INVALID_ARG
+    assert lib.cmpext3_gemm_f32(0x1000, 64, 0x2000, 64, 0x3000, 60, 64, 64, 64, None) == cabi.ERR_INVALID_ARG
+    assert lib.cmpext3_gemm_f32(0x1000, 64, 0x2000, 64, None, 64, 64, 64, 64, None) == cabi.ERR_INVALID_ARG
 
 
 def test_workspace_size_query():

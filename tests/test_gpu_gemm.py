@@ -262,6 +262,29 @@ def test_c_abi_matches_binding(dtype):
         assert err_vs_oracle(c, a, b, dtype) <= O.TOLERANCE[dtype]
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_c_abi_strided_views(dtype):
+    """cmpext3_gemm_{f16,bf16,f32} on row-pitched views: A and B are column slices of
+    wider matrices and C is written into a slice of a wider buffer, whose other
+    columns must stay untouched; same bits as the binding on contiguous copies."""
+    for M, N, K in [(300, 200, 72), (16, 512, 256), (33, 41, 17), (520, 1000, 264)]:
+        a, b = O.make_inputs(dtype, M, N, K, "normal", 0.1, M + N)
+        pad = 8 if K % 8 == 0 and N % 8 == 0 else 5  # odd pitches go to the generic kernel
+        A = torch.zeros(M, K + pad, dtype=DT[dtype], device="cuda")
+        B = torch.zeros(K, N + pad, dtype=DT[dtype], device="cuda")
+        A[:, :K] = a.cuda()
+        B[:, :N] = b.cuda()
+        C = torch.full((M, N + 3 * pad), 7.0, dtype=DT[dtype], device="cuda")
+        st = cabi.gemm_strided(CODE[dtype], A, K + pad, B, N + pad, C, N + 3 * pad, M, N, K)
+        assert st == cabi.OK
+        torch.cuda.synchronize()
+        assert torch.all(C[:, N:] == 7.0)
+        out = C[:, :N]
+        assert err_vs_oracle(out, a, b, dtype) <= O.TOLERANCE[dtype]
+        if pad == 8 and cabi.workspace_size(CODE[dtype], cabi.B_KN, M, N, K) == 0:
+            assert torch.equal(out, MATMUL[dtype](a.cuda(), b.cuda()))
+
+
 def test_runs_on_current_stream_and_is_deterministic():
     a, b = O.make_inputs("fp16", 1024, 1024, 1024, "normal", 1 / 32, 0)
     ag, bg = a.cuda(), b.cuda()
