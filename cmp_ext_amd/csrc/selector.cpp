@@ -112,7 +112,14 @@ int make_plan(const Request& r, Plan* plan) {
     const bool fast = r.align >= 16 && r.K % 8 == 0 && r.lda % 8 == 0 && r.ldb % 8 == 0 &&
                       r.ldc % 4 == 0 && (r.layout == kNK || r.N % 8 == 0) &&
                       (!batched || (r.stride_a % 8 == 0 && r.stride_b % 8 == 0 && r.stride_c % 4 == 0));
-    if (skinny_ok) {
+    // With M <= 64 the skinny kernels pay off only where the GPU would otherwise
+    // starve: once 128-column tiles alone give every CU one (N >= 32768, or a
+    // batch of such products, e.g. a 1x1 convolution over many pixels), the tiled
+    // kernel streams B faster (MI355X, 128x128 tile vs unsplit skinny kernel:
+    // 64x1048576x128 118 vs 237 us, 16x262144x512 48 vs 67 us, 64x32768x128 5.5
+    // vs 8.3 us).
+    const bool skinny_tiles_enough = fast && cdiv(r.N, 128) * r.batch >= kNumCUs;
+    if (skinny_ok && !skinny_tiles_enough) {
       p.mb = (int)std::max<int64_t>(1, cdiv(r.M, 16));
       p.bm = 16 * p.mb;
       // Wide strips (128 columns: full 256-byte row segments, the faster HBM

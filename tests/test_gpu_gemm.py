@@ -75,6 +75,8 @@ def test_generic_ragged(dtype, M, N, K):
     (130, 8, 8, "tile128x128"),
     (2048, 4096, 1000, "tile128x128"),   # two workgroups per CU
     (1000, 1000, 776, "tile128x128"),    # ragged, K not a multiple of 64
+    (64, 32768, 128, "tile128x128"),     # M <= 64 with 256 column tiles
+    (16, 32768, 264, "tile128x128"),
     (4000, 4088, 1000, "tile256x256"),   # ragged 256x256 tiles
     (4000, 14000, 520, "tile256x224"),   # ragged 256x224 tiles
 ])

@@ -17,6 +17,8 @@ K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKI
     (cabi.F16, 1024, 1024, 1024, K_TILE128),      # small: more tiles wanted
     (cabi.BF16, 64, 4096, 4096, K_SKINNY),
     (cabi.BF16, 65, 4096, 4096, K_TILE128),
+    (cabi.F16, 16, 32768, 4096, K_TILE128),       # M <= 64 but 256 column tiles: tiled beats skinny
+    (cabi.F16, 64, 32768, 128, K_TILE128),
 ])
 def test_config_kernel_choice(dtype, M, N, K, expect):
     kid, desc = cabi.plan(dtype, cabi.B_KN, M, N, K)
@@ -29,10 +31,18 @@ def test_skinny_wide_needs_workspace():
     assert kid == K_SKINNY_WIDE and "splits=4" in desc and "ksplit=2048" in desc and "grid=1x256x1" in desc
     kid, _ = cabi.plan(cabi.F16, cabi.B_KN, 16, 8192, 8192, workspace_bytes=need - 1)
     assert kid == K_SKINNY                      # too little workspace: narrow strips, no split
-    kid, desc = cabi.plan(cabi.BF16, cabi.B_KN, 16, 32768, 4096)
-    assert kid == K_SKINNY_WIDE and "splits=1" in desc   # 256 strips: no split, no workspace
+    kid, desc = cabi.plan(cabi.BF16, cabi.B_KN, 16, 25600, 4096)
+    assert kid == K_SKINNY_WIDE and "splits=1" in desc   # 200 strips: no split, no workspace
     kid, _ = cabi.plan(cabi.F16, cabi.B_KN, 17, 200, 72, workspace_bytes=1 << 30)
     assert kid == K_SKINNY                      # tiny grid either way: narrow has more workgroups
+
+
+def test_skinny_m_batches_with_many_tiles_go_tiled():
+    # a 1x1 convolution over 64 images of 128x128 pixels: C_out = 64 rows, 128 column tiles each
+    kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 64, 16384, 128, batch=64)
+    assert kid == K_TILE128, desc
+    kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 64, 16384, 128, batch=1)
+    assert kid in (K_SKINNY, K_SKINNY_WIDE), desc       # 128 tiles alone would leave CUs idle
 
 
 def test_skinny_parameters():
