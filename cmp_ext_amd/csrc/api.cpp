@@ -37,6 +37,7 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
     case kTile256x256:
     case kTile256x224:
     case kTile128x128:
+    case kTile64x256:
       return dtype == kF16 ? launch_tile_f16(plan.kernel, lay, p, grid, s)
                            : launch_tile_bf16(plan.kernel, lay, p, grid, s);
     case kSkinny:

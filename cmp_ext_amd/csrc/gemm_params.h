@@ -26,8 +26,8 @@ struct GemmParams {
 
 // Every kernel the library can launch.  The selector returns one of these.
 enum KernelId : int {
-  kTile256x256 = 0,   // f16/bf16 MFMA 32x32x16, 4 waves of 128x128, LDS-DMA ring
-  kTile256x224 = 1,   // same, 4 waves of 64x224 (N tiles of 224)
+  kTile256x256 = 0,   // f16/bf16 MFMA 16x16x32, 8 waves of 64x128, LDS-DMA ring
+  kTile256x224 = 1,   // same, 8 waves of 64x112 (N tiles of 224)
   kTile128x128 = 2,   // same, 4 waves of 64x64, two workgroups per CU
   kSkinny = 3,        // f16/bf16, M <= 64: 32-column strips through an LDS-DMA ring
   kF32Tile128 = 4,    // fp32 MFMA 16x16x4, 128x128 tile, 4-byte LDS-DMA ring
@@ -35,7 +35,8 @@ enum KernelId : int {
   kGeneric16 = 6,     // f16/bf16 any shape and alignment (element loads)
   kSkinnyWide = 7,    // f16/bf16, M <= 64: 128-column strips, K split over workgroups
   kF32Tile96x64 = 8,  // fp32, 96x64 tile
-  kNumKernels = 9
+  kTile64x256 = 9,    // f16/bf16 MFMA 16x16x32, 4 waves of 64x64, two workgroups per CU (M <= 64, short K)
+  kNumKernels = 10
 };
 
 }  // namespace cmpext3

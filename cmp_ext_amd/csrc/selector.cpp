@@ -67,6 +67,7 @@ const char* kernel_name(KernelId id) {
     case kTile256x256: return "tile256x256";
     case kTile256x224: return "tile256x224";
     case kTile128x128: return "tile128x128";
+    case kTile64x256: return "tile64x256";
     case kSkinny: return "skinny";
     case kSkinnyWide: return "skinny_wide";
     case kF32Tile128: return "f32tile128x128";
@@ -145,6 +146,14 @@ int make_plan(const Request& r, Plan* plan) {
         p.kernel = kSkinny;
         p.bn = 32;
       }
+    } else if (fast && r.M <= 64 && r.K <= 1024 && cdiv(r.N, 256) * r.batch >= kNumCUs) {
+      // Short-K products with few rows and many columns are HBM-bound; 64-row tiles
+      // waste no MFMA rows and keep more loads in flight per CU (MI355X, 64x256 vs
+      // 128x128: 64x1048576x128 103 vs 122 us, 32x131072x256 14.4 vs 17.3 us; at
+      // K >= 2048 the 128x128 tile or the skinny kernel is faster).
+      p.kernel = kTile64x256;
+      p.bm = 64;
+      p.bn = 256;
     } else if (fast) {
       const Candidate* c = pick(kTiles16, 3, r.M, r.N, r.batch);
       p.kernel = c->id;

@@ -1,6 +1,7 @@
 // Instantiations of the tiled MFMA GEMM for bf16: 256 x 256 and 256 x 224
 // tiles with 8 waves and one workgroup per CU (128 KB of LDS); 128 x 128 tiles
-// with 4 waves and two workgroups per CU.
+// with 4 waves and two workgroups per CU; 64 x 256 tiles (M <= 64, short K) with
+// 4 waves and two workgroups per CU.
 #include "kernels.h"
 #include "tile16_kernel.h"
 
@@ -17,6 +18,9 @@ hipError_t launch(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s) {
       break;
     case kTile128x128:
       launch_tile16<__bf16, KN, 128, 128, 2, 2, 2>(p, grid, s);
+      break;
+    case kTile64x256:
+      launch_tile16<__bf16, KN, 64, 256, 1, 4, 2>(p, grid, s);
       break;
     default:
       return hipErrorInvalidValue;

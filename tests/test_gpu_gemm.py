@@ -23,7 +23,7 @@ pytestmark = pytest.mark.gpu
 DT = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
 CODE = {"fp16": cabi.F16, "bf16": cabi.BF16, "fp32": cabi.F32}
 MATMUL = {"fp16": cmpext3.fp16_matmul, "bf16": cmpext3.bf16_matmul, "fp32": cmpext3.fp32_matmul}
-KERNEL_NAMES = ["tile256x256", "tile256x224", "tile128x128", "skinny", "skinny_wide", "f32tile128x128",
+KERNEL_NAMES = ["tile256x256", "tile256x224", "tile128x128", "tile64x256", "skinny", "skinny_wide", "f32tile128x128",
                 "f32tile64x64", "f32tile96x64", "generic64x64"]
 SEEN_KERNELS = set()
 
@@ -77,6 +77,8 @@ def test_generic_ragged(dtype, M, N, K):
     (1000, 1000, 776, "tile128x128"),    # ragged, K not a multiple of 64
     (64, 32768, 128, "tile128x128"),     # M <= 64 with 256 column tiles
     (16, 32768, 264, "tile128x128"),
+    (64, 65536, 512, "tile64x256"),      # M <= 64, short K, 256 tiles of 256 columns
+    (40, 70000, 200, "tile64x256"),      # ragged rows, columns and K
     (4000, 4088, 1000, "tile256x256"),   # ragged 256x256 tiles
     (4000, 14000, 520, "tile256x224"),   # ragged 256x224 tiles
 ])

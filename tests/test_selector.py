@@ -3,7 +3,7 @@ import pytest
 
 from cmp_ext_amd import cabi
 
-K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKINNY_WIDE, K_F32_96 = range(9)
+K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKINNY_WIDE, K_F32_96, K_TILE64 = range(10)
 
 
 @pytest.mark.parametrize("dtype,M,N,K,expect", [
@@ -19,6 +19,8 @@ K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKI
     (cabi.BF16, 65, 4096, 4096, K_TILE128),
     (cabi.F16, 16, 32768, 4096, K_TILE128),       # M <= 64 but 256 column tiles: tiled beats skinny
     (cabi.F16, 64, 32768, 128, K_TILE128),
+    (cabi.F16, 64, 65536, 512, K_TILE64),         # ... and with short K and 256 tiles of 256 columns
+    (cabi.BF16, 32, 131072, 256, K_TILE64),
 ])
 def test_config_kernel_choice(dtype, M, N, K, expect):
     kid, desc = cabi.plan(dtype, cabi.B_KN, M, N, K)
@@ -40,7 +42,7 @@ def test_skinny_wide_needs_workspace():
 def test_skinny_m_batches_with_many_tiles_go_tiled():
     # a 1x1 convolution over 64 images of 128x128 pixels: C_out = 64 rows, 128 column tiles each
     kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 64, 16384, 128, batch=64)
-    assert kid == K_TILE128, desc
+    assert kid == K_TILE64, desc
     kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 64, 16384, 128, batch=1)
     assert kid in (K_SKINNY, K_SKINNY_WIDE), desc       # 128 tiles alone would leave CUs idle
 
