@@ -200,17 +200,22 @@ __device__ __forceinline__ void dma128_geom(int slot, int lane, int& row, int& c
 }
 
 // ---------------------------------------------------------------------------
-// Tile order.  The dispatcher hands workgroup w to XCD w % 8; consecutive
-// logical tiles are given to the same XCD so that its L2 sees a compact block
-// of A rows and B columns, and inside that order tiles are grouped
-// `group_m` rows at a time (column-major within the group).
+// Tile order.  The dispatcher hands workgroup w (x fastest, then z) to XCD
+// w % 8; consecutive logical tiles -- batch entry by batch entry -- are given to
+// the same XCD so that its L2 sees a compact block of A rows and B columns (and
+// whole batch entries of a batched product), and inside an entry tiles are
+// grouped `group_m` rows at a time (column-major within the group).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void tile_coords(int wg, int tiles_m, int tiles_n, int group_m,
-                                            int& tm, int& tn) {
-  const int total = tiles_m * tiles_n;
-  const int xcd = wg & 7, local = wg >> 3;
-  const int base = total >> 3, rem = total & 7;
-  const int t = xcd * base + (xcd < rem ? xcd : rem) + local;
+__device__ __forceinline__ void tile_coords(int x, int z, int nz, int tiles_m, int tiles_n, int group_m,
+                                            int& tm, int& tn, int& bz) {
+  const int tiles = tiles_m * tiles_n;
+  const int64_t total = (int64_t)tiles * nz;
+  const int64_t wg = x + (int64_t)tiles * z;
+  const int xcd = (int)(wg & 7);
+  const int64_t base = total >> 3, rem = total & 7;
+  const int64_t s = xcd * base + (xcd < rem ? xcd : rem) + (wg >> 3);
+  bz = (int)(s / tiles);
+  const int t = (int)(s - (int64_t)bz * tiles);
   const int per_group = group_m * tiles_n;
   const int g = t / per_group;
   const int first_m = g * group_m;

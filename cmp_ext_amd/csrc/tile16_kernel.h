@@ -112,11 +112,12 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
   const int wm = wave / WN, wn = wave % WN;
 
   int tm, tn;
-  tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+  int bzi;
+  tile_coords(blockIdx.x, blockIdx.z, gridDim.z, p.tiles_m, p.tiles_n, p.group_m, tm, tn, bzi);
   const int m0 = tm * BM, n0 = tn * BN;
   const int M = p.M, N = p.N, K = p.K;
   const int64_t lda = p.lda, ldb = p.ldb;
-  const int64_t bz = blockIdx.z;
+  const int64_t bz = bzi;
   const T* Abase = (const T*)p.A + bz * p.stride_a + (int64_t)m0 * lda;
   const T* Bbase = KN ? (const T*)p.B + bz * p.stride_b + n0 : (const T*)p.B + bz * p.stride_b + (int64_t)n0 * ldb;
 
