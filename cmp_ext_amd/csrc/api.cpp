@@ -29,7 +29,7 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
   const BLayout lay = (BLayout)layout;
   switch (plan.kernel) {
     case kSkinnyWide: {
-      hipError_t e = launch_skinny_wide((DType)dtype, plan.mb, p, (float*)ws, plan.splits, plan.ksplit, grid, s);
+      hipError_t e = launch_skinny_wide((DType)dtype, lay, plan.mb, p, (float*)ws, plan.splits, plan.ksplit, grid, s);
       if (e == hipSuccess && plan.splits > 1)
         e = launch_skinny_reduce((DType)dtype, p, (const float*)ws, plan.splits, (int)grid.z, s);
       return e;

@@ -107,7 +107,7 @@ int make_plan(const Request& r, Plan* plan) {
     p.bm = c->bm;
     p.bn = c->bn;
   } else {
-    const bool skinny_ok = r.layout == kKN && r.M <= 64 && r.align >= 16 && r.K % 8 == 0 &&
+    const bool skinny_ok = r.M <= 64 && r.align >= 16 && r.K % 8 == 0 &&
                            r.lda % 8 == 0 && r.N % 8 == 0 && r.ldb % 8 == 0 &&
                            (!batched || (r.stride_a % 8 == 0 && r.stride_b % 8 == 0));
     const bool fast = r.align >= 16 && r.K % 8 == 0 && r.lda % 8 == 0 && r.ldb % 8 == 0 &&
@@ -136,12 +136,21 @@ int make_plan(const Request& r, Plan* plan) {
       splits = std::min<int64_t>(splits, std::max<int64_t>(1, r.K / 256));
       const int64_t need = splits > 1 ? splits * chunk * r.M * r.N * 4 : 0;
       const int64_t wide_wgs = strips * splits * chunk, narrow_wgs = cdiv(r.N, 32) * chunk;
-      if (need <= r.ws_bytes && 2 * wide_wgs >= std::min<int64_t>(narrow_wgs, 256)) {
+      // B given as [N, K] (a Linear weight) has only the wide kernel: unsplit
+      // when the workspace is missing.
+      const bool nk = r.layout == kNK;
+      if (need <= r.ws_bytes && (nk || 2 * wide_wgs >= std::min<int64_t>(narrow_wgs, 256))) {
         p.kernel = kSkinnyWide;
         p.bn = 128;
         p.splits = (int)splits;
         p.ksplit = (int)(cdiv(cdiv(r.K, splits), 64) * 64);
         p.ws_bytes = need;
+      } else if (nk) {
+        p.kernel = kSkinnyWide;
+        p.bn = 128;
+        p.splits = 1;
+        p.ksplit = (int)std::max<int64_t>(64, cdiv(r.K, 64) * 64);
+        p.ws_bytes = 0;
       } else {
         p.kernel = kSkinny;
         p.bn = 32;

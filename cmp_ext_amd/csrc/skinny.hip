@@ -1,4 +1,5 @@
-// Instantiations of the skinny-M GEMM (M <= 64, B is [K, N]).
+// Instantiations of the skinny-M GEMM (M <= 64; B is [K, N], or [N, K] for the
+// split-K wide kernel).
 #include "kernels.h"
 #include "skinny_kernel.h"
 #include "skinny_wide_kernel.h"
@@ -26,24 +27,28 @@ hipError_t launch_skinny(DType dt, int mb, const GemmParams& p, dim3 grid, hipSt
 }
 
 namespace {
-template <typename T>
+template <typename T, bool KN>
 hipError_t launch_wide(int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid, hipStream_t s) {
   const dim3 block(256);
   switch (mb) {
-    case 1: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 1>), grid, block, 0, s, p, ws, splits, ksplit); break;
-    case 2: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 2>), grid, block, 0, s, p, ws, splits, ksplit); break;
-    case 3: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 3>), grid, block, 0, s, p, ws, splits, ksplit); break;
-    case 4: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 4>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    case 1: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 1, KN>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    case 2: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 2, KN>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    case 3: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 3, KN>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    case 4: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 4, KN>), grid, block, 0, s, p, ws, splits, ksplit); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 }  // namespace
 
-hipError_t launch_skinny_wide(DType dt, int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid,
-                              hipStream_t s) {
-  if (dt == kF16) return launch_wide<_Float16>(mb, p, ws, splits, ksplit, grid, s);
-  if (dt == kBF16) return launch_wide<__bf16>(mb, p, ws, splits, ksplit, grid, s);
+hipError_t launch_skinny_wide(DType dt, BLayout lay, int mb, const GemmParams& p, float* ws, int splits, int ksplit,
+                              dim3 grid, hipStream_t s) {
+  if (dt == kF16)
+    return lay == kKN ? launch_wide<_Float16, true>(mb, p, ws, splits, ksplit, grid, s)
+                      : launch_wide<_Float16, false>(mb, p, ws, splits, ksplit, grid, s);
+  if (dt == kBF16)
+    return lay == kKN ? launch_wide<__bf16, true>(mb, p, ws, splits, ksplit, grid, s)
+                      : launch_wide<__bf16, false>(mb, p, ws, splits, ksplit, grid, s);
   return hipErrorInvalidValue;
 }
 

@@ -197,7 +197,9 @@ def test_fp16_overflow_matches_rounding():
 # ------------------------------------------------------- layouts, views, bias
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
 @pytest.mark.parametrize("shape", [(2, 150, 72, 200), (1, 4096, 4096, 4096), (3, 7, 40, 12), (1, 16, 64, 64),
-                                   (1, 2048, 512, 1004), (1, 4096, 512, 3588), (2, 2048, 1024, 3588)])
+                                   (1, 2048, 512, 1004), (1, 4096, 512, 3588), (2, 2048, 1024, 3588),
+                                   (1, 16, 14336, 4096), (1, 1, 4096, 4096), (2, 16, 520, 1000),
+                                   (1, 64, 2048, 256)])  # the last four: decode shapes, skinny kernel on W [N,K]
 def test_linear_with_bias(dtype, shape):
     Bt, S, K, N = shape
     g = torch.Generator().manual_seed(sum(shape))
@@ -212,6 +214,26 @@ def test_linear_with_bias(dtype, shape):
     assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
     out_nb = cmpext3.linear(x.cuda(), w.cuda())
     assert O.rel_frobenius(O.to_f64(out_nb.cpu()), O.linear_f64(O.to_f64(x), O.to_f64(w))) <= O.TOLERANCE[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_skinny_linear_weight_with_and_without_workspace(dtype):
+    """Decode-shaped Linear: W [N, K] through the skinny kernel, split over K with a
+    workspace (binding) and unsplit without one (C ABI): both against the oracle."""
+    M, N, K = 16, 4096, 4096
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    w = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    ref = O.linear_f64(O.to_f64(x), O.to_f64(w))
+    out = cmpext3.linear(x.cuda(), w.cuda())
+    kid, desc = cabi.plan(CODE[dtype], cabi.B_NK, M, N, K)
+    assert "skinny_wide" in desc and "splits=1 " in desc, desc
+    SEEN_KERNELS.add("skinny_wide")
+    c = torch.empty(M, N, dtype=DT[dtype], device="cuda")
+    assert cabi.gemm_ex(CODE[dtype], cabi.B_NK, x.cuda(), K, 0, w.cuda(), K, 0, c, N, 0, None, M, N, K) == cabi.OK
+    torch.cuda.synchronize()
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    assert O.rel_frobenius(O.to_f64(c.cpu()), ref) <= O.TOLERANCE[dtype]
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])

@@ -47,6 +47,16 @@ def test_skinny_m_batches_with_many_tiles_go_tiled():
     assert kid in (K_SKINNY, K_SKINNY_WIDE), desc       # 128 tiles alone would leave CUs idle
 
 
+def test_skinny_linear_weight_layout():
+    # decode-shaped Linear (W is [N, K]): split-K wide kernel with a workspace, unsplit without
+    need = cabi.workspace_size(cabi.F16, cabi.B_NK, 16, 4096, 14336)
+    assert need == 8 * 16 * 4096 * 4
+    kid, desc = cabi.plan(cabi.F16, cabi.B_NK, 16, 4096, 14336, workspace_bytes=need)
+    assert kid == K_SKINNY_WIDE and "splits=8" in desc, desc
+    kid, desc = cabi.plan(cabi.BF16, cabi.B_NK, 16, 4096, 14336)
+    assert kid == K_SKINNY_WIDE and "splits=1 " in desc, desc
+
+
 def test_skinny_parameters():
     kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 16, 8192, 8192)
     assert kid == K_SKINNY
@@ -64,7 +74,7 @@ def test_skinny_parameters():
     (16, 63, 64, cabi.B_KN, 16, K_GENERIC),     # skinny needs N % 8 == 0
     (16, 100, 64, cabi.B_KN, 16, K_GENERIC),
     (16, 64, 60, cabi.B_KN, 16, K_GENERIC),     # skinny needs K % 8 == 0
-    (16, 64, 64, cabi.B_NK, 16, K_TILE128),     # skinny is KN only
+    (16, 64, 64, cabi.B_NK, 16, K_SKINNY_WIDE),  # [N,K] B (Linear weight): the wide kernel, unsplit
 ])
 def test_alignment_fallbacks(M, N, K, layout, align, expect):
     kid, desc = cabi.plan(cabi.F16, layout, M, N, K, align=align)
