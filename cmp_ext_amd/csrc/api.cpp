@@ -29,7 +29,7 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
   const BLayout lay = (BLayout)layout;
   switch (plan.kernel) {
     case kSkinnyWide: {
-      hipError_t e = launch_skinny_wide((DType)dtype, lay, plan.mb, p, (float*)ws, plan.splits, plan.ksplit, grid, s);
+      hipError_t e = launch_skinny_wide((DType)dtype, plan.mb, p, (float*)ws, plan.splits, plan.ksplit, grid, s);
       if (e == hipSuccess && plan.splits > 1)
         e = launch_skinny_reduce((DType)dtype, p, (const float*)ws, plan.splits, (int)grid.z, s);
       return e;
@@ -42,6 +42,8 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
                            : launch_tile_bf16(plan.kernel, lay, p, grid, s);
     case kSkinny:
       return launch_skinny((DType)dtype, plan.mb, p, grid, s);
+    case kSkinnyNK:
+      return launch_skinny_nk((DType)dtype, plan.mb, plan.bn, p, grid, s);
     case kF32Tile128:
     case kF32Tile64:
     case kF32Tile96x64:

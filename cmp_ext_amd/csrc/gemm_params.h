@@ -36,7 +36,8 @@ enum KernelId : int {
   kSkinnyWide = 7,    // f16/bf16, M <= 64: 128-column strips, K split over workgroups
   kF32Tile96x64 = 8,  // fp32, 96x64 tile
   kTile64x256 = 9,    // f16/bf16 MFMA 16x16x32, 4 waves of 64x64, two workgroups per CU (M <= 64, short K)
-  kNumKernels = 10
+  kSkinnyNK = 10,     // f16/bf16, M <= 64, B is [N,K]: 16- or 32-row strips of W, all of K per workgroup
+  kNumKernels = 11
 };
 
 }  // namespace cmpext3

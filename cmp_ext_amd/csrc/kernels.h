@@ -11,8 +11,9 @@ namespace cmpext3 {
 hipError_t launch_tile_f16(KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
 hipError_t launch_tile_bf16(KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
 hipError_t launch_skinny(DType dt, int mb, const GemmParams& p, dim3 grid, hipStream_t s);
-hipError_t launch_skinny_wide(DType dt, BLayout lay, int mb, const GemmParams& p, float* ws, int splits, int ksplit,
-                              dim3 grid, hipStream_t s);
+hipError_t launch_skinny_nk(DType dt, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_skinny_wide(DType dt, int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid,
+                              hipStream_t s);
 hipError_t launch_skinny_reduce(DType dt, const GemmParams& p, const float* ws, int splits, int batch,
                                 hipStream_t s);
 hipError_t launch_f32(KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);

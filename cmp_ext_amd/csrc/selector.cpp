@@ -70,6 +70,7 @@ const char* kernel_name(KernelId id) {
     case kTile64x256: return "tile64x256";
     case kSkinny: return "skinny";
     case kSkinnyWide: return "skinny_wide";
+    case kSkinnyNK: return "skinny_nk";
     case kF32Tile128: return "f32tile128x128";
     case kF32Tile64: return "f32tile64x64";
     case kF32Tile96x64: return "f32tile96x64";
@@ -120,7 +121,14 @@ int make_plan(const Request& r, Plan* plan) {
     // 64x1048576x128 118 vs 237 us, 16x262144x512 48 vs 67 us, 64x32768x128 5.5
     // vs 8.3 us).
     const bool skinny_tiles_enough = fast && cdiv(r.N, 128) * r.batch >= kNumCUs;
-    if (skinny_ok && !skinny_tiles_enough) {
+    if (skinny_ok && !skinny_tiles_enough && r.layout == kNK) {
+      // B is [N, K] (a Linear weight): strips of W rows over all of K; 16-row
+      // strips when 32-row ones would leave CUs idle.
+      p.mb = (int)std::max<int64_t>(1, cdiv(r.M, 16));
+      p.bm = 16 * p.mb;
+      p.kernel = kSkinnyNK;
+      p.bn = cdiv(r.N, 32) * std::min<int64_t>(r.batch, 65535) >= kNumCUs ? 32 : 16;
+    } else if (skinny_ok && !skinny_tiles_enough) {
       p.mb = (int)std::max<int64_t>(1, cdiv(r.M, 16));
       p.bm = 16 * p.mb;
       // Wide strips (128 columns: full 256-byte row segments, the faster HBM
@@ -136,21 +144,12 @@ int make_plan(const Request& r, Plan* plan) {
       splits = std::min<int64_t>(splits, std::max<int64_t>(1, r.K / 256));
       const int64_t need = splits > 1 ? splits * chunk * r.M * r.N * 4 : 0;
       const int64_t wide_wgs = strips * splits * chunk, narrow_wgs = cdiv(r.N, 32) * chunk;
-      // B given as [N, K] (a Linear weight) has only the wide kernel: unsplit
-      // when the workspace is missing.
-      const bool nk = r.layout == kNK;
-      if (need <= r.ws_bytes && (nk || 2 * wide_wgs >= std::min<int64_t>(narrow_wgs, 256))) {
+      if (need <= r.ws_bytes && 2 * wide_wgs >= std::min<int64_t>(narrow_wgs, 256)) {
         p.kernel = kSkinnyWide;
         p.bn = 128;
         p.splits = (int)splits;
         p.ksplit = (int)(cdiv(cdiv(r.K, splits), 64) * 64);
         p.ws_bytes = need;
-      } else if (nk) {
-        p.kernel = kSkinnyWide;
-        p.bn = 128;
-        p.splits = 1;
-        p.ksplit = (int)std::max<int64_t>(64, cdiv(r.K, 64) * 64);
-        p.ws_bytes = 0;
       } else {
         p.kernel = kSkinny;
         p.bn = 32;
@@ -176,7 +175,7 @@ int make_plan(const Request& r, Plan* plan) {
     }
   }
   if (p.splits == 0) p.splits = 1;
-  if (p.kernel == kSkinny || p.kernel == kSkinnyWide) {
+  if (p.kernel == kSkinny || p.kernel == kSkinnyWide || p.kernel == kSkinnyNK) {
     p.tiles_m = 1;
     p.tiles_n = (int)cdiv(r.N, p.bn) * (p.kernel == kSkinnyWide ? p.splits : 1);
   } else {
@@ -194,7 +193,7 @@ std::string describe(const Request& r, const Plan& p) {
            kernel_name(p.kernel), dt[r.dtype], r.layout == kKN ? "KN" : "NK", p.bm, p.bn, p.tiles_m,
            p.tiles_n, (long long)r.batch, p.threads);
   std::string s(buf);
-  if (p.kernel == kSkinny || p.kernel == kSkinnyWide) {
+  if (p.kernel == kSkinny || p.kernel == kSkinnyWide || p.kernel == kSkinnyNK) {
     snprintf(buf, sizeof buf, " mb=%d", p.mb);
     s += buf;
   }

@@ -188,4 +188,148 @@ __global__ void __launch_bounds__(256) gemm_skinny_narrow_kernel(const GemmParam
   }
 }
 
+// Skinny-M product with B given as [N, K] (a Linear weight used as W^T, decode
+// shapes such as x[16, 4096] * W[14336, 4096]^T): each workgroup owns SW rows of W
+// (SW output columns) and all of K.  W rows are K-contiguous, so a stage holds KS k
+// of each row -- 2*KS contiguous bytes per row per load, which keeps HBM reads in
+// long runs -- stored like A (rows of 2*KS bytes, 16-byte chunks XORed with row%16)
+// and read with ds_read_b128 straight into the MFMA's first operand.  As above,
+// the stage's 32-deep k-blocks are split over the 4 waves and the partial sums
+// reduced in LDS at the end; no workspace, no second launch.
+template <int MB, int SW, int KS_>
+struct SkinnyNKShape {
+  static constexpr int KS = KS_;
+  static constexpr int PITCH = KS * 2;             // bytes per LDS row (W and A alike)
+  static constexpr int W_BYTES = SW * PITCH;
+  static constexpr int A_BYTES = MB * 16 * PITCH;
+  static constexpr int STAGE = W_BYTES + A_BYTES;
+  static constexpr int NS = (160 * 1024) / STAGE > 8 ? 8 : (160 * 1024) / STAGE;
+  static constexpr int W_DMA = W_BYTES / 4096;  // 1 KB LDS-DMA loads per wave per stage
+  static constexpr int A_DMA = A_BYTES / 4096;
+  static constexpr int DMA = W_DMA + A_DMA;
+  static constexpr int KB = KS / 32 / 4;        // 32-deep k-blocks per wave per stage
+  static_assert(W_BYTES % 4096 == 0 && A_BYTES % 4096 == 0 && KB >= 1, "whole DMA loads per wave");
+  static_assert(NS >= 3 && (NS - 2) * DMA <= 63, "ring depth / vmcnt range");
+  static_assert(4 * MB * 16 * SW * 4 <= NS * STAGE, "reduction fits the ring");
+};
+
+template <typename T, int MB, int SW, int KS>
+__global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p) {
+  using S = SkinnyNKShape<MB, SW, KS>;
+  constexpr int NS = S::NS;
+  constexpr int NB = SW / 16;  // 16-column blocks per strip
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * S::STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int strip = strip_order(blockIdx.x, gridDim.x);
+  const int n0 = strip * SW;
+  const int M = p.M, N = p.N, K = p.K;
+  const int64_t bz = blockIdx.z;
+  const int64_t lda = p.lda, ldb = p.ldb;
+  const T* Ab = (const T*)p.A + bz * p.stride_a;
+  const T* Wb = (const T*)p.B + bz * p.stride_b + (int64_t)n0 * ldb;
+
+  // ---- DMA sources: rows of PITCH bytes, chunk c of row r stored at chunk c ^ (r % 16) ----
+  auto geom = [&](int piece, int& row, int& chunk) {
+    const int pos = piece * 1024 + 16 * lane;
+    row = pos / S::PITCH;
+    chunk = ((pos % S::PITCH) >> 4) ^ (row & 15);
+  };
+  uint32_t w_off[S::W_DMA];
+  int w_k[S::W_DMA];
+#pragma unroll
+  for (int i = 0; i < S::W_DMA; ++i) {
+    int row, chunk;
+    geom(wave * S::W_DMA + i, row, chunk);
+    w_off[i] = (n0 + row < N) ? (uint32_t)(row * ldb + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
+    w_k[i] = 8 * chunk;
+  }
+  uint32_t a_off[S::A_DMA];
+  int a_k[S::A_DMA];
+#pragma unroll
+  for (int i = 0; i < S::A_DMA; ++i) {
+    int row, chunk;
+    geom(wave * S::A_DMA + i, row, chunk);
+    a_off[i] = (row < M) ? (uint32_t)(row * lda + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
+    a_k[i] = 8 * chunk;
+  }
+  auto load_stage = [&](int st) {
+    const int k0 = st * S::KS;
+    const uint32_t dst = lds_addr(smem) + (uint32_t)((st % NS) * S::STAGE);
+    const int krem = K - k0;
+    const i32x4 rw = make_rsrc_sgpr(Wb + k0);
+    const i32x4 ra = make_rsrc_sgpr(Ab + k0);
+#pragma unroll
+    for (int i = 0; i < S::W_DMA; ++i)
+      dma_load16(rw, w_k[i] < krem ? w_off[i] : kBufOOB, dst + (wave * S::W_DMA + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < S::A_DMA; ++i)
+      dma_load16(ra, a_k[i] < krem ? a_off[i] : kBufOOB, dst + S::W_BYTES + (wave * S::A_DMA + i) * 1024);
+  };
+
+  // ---- fragments: lane (c = l%16, g = l/16) ----
+  // first MFMA operand: W row 16h + c (column n0 + 16h + c of C) at k = kb + 8g .. +7
+  // second operand:     A row 16mb + c at the same k
+  const int c = lane & 15, g = lane >> 4;
+  f32x4 acc[NB][MB];
+#pragma unroll
+  for (int h = 0; h < NB; ++h)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[h][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute_stage = [&](int st) {
+    const unsigned char* stage = smem + (st % NS) * S::STAGE;
+#pragma unroll
+    for (int b = 0; b < S::KB; ++b) {
+      const int kc = (wave * S::KB + b) * 4 + g;  // 16-byte chunk of the lane's 8 k
+      u32x4 af[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        af[mb] = *(const u32x4*)(stage + S::W_BYTES + (16 * mb + c) * S::PITCH + 16 * (kc ^ c));
+#pragma unroll
+      for (int h = 0; h < NB; ++h) {
+        const u32x4 wf = *(const u32x4*)(stage + (16 * h + c) * S::PITCH + 16 * (kc ^ c));
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[h][mb] = Mfma<T>::mma(wf, af[mb], acc[h][mb]);
+      }
+    }
+  };
+
+  const int nst = (K + S::KS - 1) / S::KS;
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t) load_stage(t);
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 2) * S::DMA) : "memory");
+  for (int st = 0; st < nst; ++st) {
+    load_stage(st + NS - 1);
+    compute_stage(st);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"((NS - 2) * S::DMA) : "memory");
+  }
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" : : : "memory");
+
+  // ---- reduce the 4 waves' partial sums through LDS (the ring is free) ----
+  // acc[h][mb][r] = C[16*mb + c][n0 + 16*h + 4*g + r]
+  float* red = (float*)smem;  // [wave][MB*16][SW]
+#pragma unroll
+  for (int h = 0; h < NB; ++h)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[(wave * MB * 16 + 16 * mb + c) * SW + 16 * h + 4 * g + r] = acc[h][mb][r];
+  __syncthreads();
+  T* Cb = (T*)p.C + bz * p.stride_c;
+  const uint16_t* bias = (const uint16_t*)p.bias;
+  for (int o = tid; o < MB * 16 * SW; o += 256) {
+    const int row = o / SW, col = o % SW;
+    const int n = n0 + col;
+    if (row >= M || n >= N) continue;
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) s += red[(w * MB * 16 + row) * SW + col];
+    if (bias) s += from_bits<T>(bias[p.bias_row ? row : n]);
+    ((uint16_t*)(Cb + (int64_t)row * p.ldc))[n] = to_bits<T>(s);
+  }
+}
+
 }  // namespace cmpext3

@@ -46,10 +46,7 @@ __device__ __forceinline__ uint32_t wide_off(int k, int seg) {
   return (uint32_t)(k * 256 + ((seg ^ wide_swz(k)) << 5));
 }
 
-// KN: B is [K, N] (matmul, bmm).  Otherwise B is [N, K] (a Linear weight, used as
-// W^T): the strip is 128 rows of W, stored like A (K-contiguous rows of 128 bytes in
-// the lds_off128 layout) and read with ds_read_b128, no transposing reads.
-template <typename T, int MB, bool KN>
+template <typename T, int MB>
 __global__ void __launch_bounds__(256) gemm_skinny_wide_kernel(const GemmParams p, float* ws, int splits,
                                                                int ksplit) {
   using S = WideShape<MB>;
@@ -68,8 +65,7 @@ __global__ void __launch_bounds__(256) gemm_skinny_wide_kernel(const GemmParams 
   const int64_t bz = blockIdx.z;
   const int64_t lda = p.lda, ldb = p.ldb;
   const T* Ab = (const T*)p.A + bz * p.stride_a + kbeg;
-  const T* Bb = KN ? (const T*)p.B + bz * p.stride_b + (int64_t)kbeg * ldb + n0
-                  : (const T*)p.B + bz * p.stride_b + (int64_t)n0 * ldb + kbeg;
+  const T* Bb = (const T*)p.B + bz * p.stride_b + (int64_t)kbeg * ldb + n0;
   const int klen = kend - kbeg;
 
   // ---- DMA sources (inverse of the LDS layouts), relative to the stage's k0 ----
@@ -77,18 +73,11 @@ __global__ void __launch_bounds__(256) gemm_skinny_wide_kernel(const GemmParams 
   int b_k[S::B_DMA];
 #pragma unroll
   for (int i = 0; i < S::B_DMA; ++i) {
-    if (KN) {
-      const int row = 4 * (wave * S::B_DMA + i) + (lane >> 4);  // 4 rows of 256 bytes per load
-      const int seg = ((lane & 15) >> 1) ^ wide_swz(row);
-      const int col = seg * 16 + (lane & 1) * 8;
-      b_off[i] = (n0 + col < N) ? (uint32_t)(row * ldb + col) * (uint32_t)sizeof(T) : kBufOOB;
-      b_k[i] = row;
-    } else {  // 8 rows of W (columns of C) of 128 bytes per load
-      int row, chunk;
-      dma128_geom(wave * S::B_DMA + i, lane, row, chunk);
-      b_off[i] = (n0 + row < N) ? (uint32_t)(row * ldb + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
-      b_k[i] = 8 * chunk;
-    }
+    const int row = 4 * (wave * S::B_DMA + i) + (lane >> 4);  // 4 rows of 256 bytes per load
+    const int seg = ((lane & 15) >> 1) ^ wide_swz(row);
+    const int col = seg * 16 + (lane & 1) * 8;
+    b_off[i] = (n0 + col < N) ? (uint32_t)(row * ldb + col) * (uint32_t)sizeof(T) : kBufOOB;
+    b_k[i] = row;
   }
   const int a_cnt = wave < (S::A_DMA_WG & 3) || (S::A_DMA_WG & 3) == 0 ? S::A_HI : S::A_LO;
   uint32_t a_off[S::A_HI];
@@ -104,7 +93,7 @@ __global__ void __launch_bounds__(256) gemm_skinny_wide_kernel(const GemmParams 
     const int k0 = st * kWideKS;
     const uint32_t dst = lds_addr(smem) + (uint32_t)((st % NS) * S::STAGE);
     const int krem = klen - k0;
-    const i32x4 rb = make_rsrc_sgpr(KN ? Bb + (int64_t)k0 * ldb : Bb + k0);
+    const i32x4 rb = make_rsrc_sgpr(Bb + (int64_t)k0 * ldb);
     const i32x4 ra = make_rsrc_sgpr(Ab + k0);
 #pragma unroll
     for (int i = 0; i < S::B_DMA; ++i)
@@ -143,18 +132,14 @@ __global__ void __launch_bounds__(256) gemm_skinny_wide_kernel(const GemmParams 
       for (int h = 0; h < 2; ++h) {
         const int seg = 2 * wave + h;
         u32x4 bf;
-        if (KN) {
 #pragma unroll
-          for (int r = 0; r < 2; ++r) {
-            const int k = kb + 8 * g + 4 * r + (c >> 2);
-            const unsigned char* q = stage + wide_off(k, seg) + 8 * (c & 3);
-            const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q);
-            const u32x2 v2 = __builtin_bit_cast(u32x2, v);
-            bf[2 * r] = v2.x;
-            bf[2 * r + 1] = v2.y;
-          }
-        } else {  // column 16 seg + c of C = row of W, k = kb + 8g .. +7
-          bf = *(const u32x4*)(stage + lds_off128(16 * seg + c, kb / 8 + g));
+        for (int r = 0; r < 2; ++r) {
+          const int k = kb + 8 * g + 4 * r + (c >> 2);
+          const unsigned char* q = stage + wide_off(k, seg) + 8 * (c & 3);
+          const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q);
+          const u32x2 v2 = __builtin_bit_cast(u32x2, v);
+          bf[2 * r] = v2.x;
+          bf[2 * r + 1] = v2.y;
         }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[h][mb] = Mfma<T>::mma(bf, af[mb], acc[h][mb]);

@@ -3,7 +3,8 @@ import pytest
 
 from cmp_ext_amd import cabi
 
-K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKINNY_WIDE, K_F32_96, K_TILE64 = range(10)
+K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKINNY_WIDE, K_F32_96, K_TILE64, \
+    K_SKINNY_NK = range(11)
 
 
 @pytest.mark.parametrize("dtype,M,N,K,expect", [
@@ -48,13 +49,13 @@ def test_skinny_m_batches_with_many_tiles_go_tiled():
 
 
 def test_skinny_linear_weight_layout():
-    # decode-shaped Linear (W is [N, K]): split-K wide kernel with a workspace, unsplit without
-    need = cabi.workspace_size(cabi.F16, cabi.B_NK, 16, 4096, 14336)
-    assert need == 8 * 16 * 4096 * 4
-    kid, desc = cabi.plan(cabi.F16, cabi.B_NK, 16, 4096, 14336, workspace_bytes=need)
-    assert kid == K_SKINNY_WIDE and "splits=8" in desc, desc
-    kid, desc = cabi.plan(cabi.BF16, cabi.B_NK, 16, 4096, 14336)
-    assert kid == K_SKINNY_WIDE and "splits=1 " in desc, desc
+    # decode-shaped Linear (W is [N, K]): strips of W rows over all of K, no workspace;
+    # 16-row strips until 32-row ones give every CU one
+    assert cabi.workspace_size(cabi.F16, cabi.B_NK, 16, 4096, 14336) == 0
+    kid, desc = cabi.plan(cabi.F16, cabi.B_NK, 16, 4096, 14336, workspace_bytes=1 << 30)
+    assert kid == K_SKINNY_NK and "tile=16x16" in desc and "grid=1x256x1" in desc, desc
+    kid, desc = cabi.plan(cabi.BF16, cabi.B_NK, 64, 14336, 4096)
+    assert kid == K_SKINNY_NK and "tile=64x32" in desc and "mb=4" in desc, desc
 
 
 def test_skinny_parameters():
@@ -74,7 +75,7 @@ def test_skinny_parameters():
     (16, 63, 64, cabi.B_KN, 16, K_GENERIC),     # skinny needs N % 8 == 0
     (16, 100, 64, cabi.B_KN, 16, K_GENERIC),
     (16, 64, 60, cabi.B_KN, 16, K_GENERIC),     # skinny needs K % 8 == 0
-    (16, 64, 64, cabi.B_NK, 16, K_SKINNY_WIDE),  # [N,K] B (Linear weight): the wide kernel, unsplit
+    (16, 64, 64, cabi.B_NK, 16, K_SKINNY_NK),   # [N,K] B (Linear weight): strips of W rows
 ])
 def test_alignment_fallbacks(M, N, K, layout, align, expect):
     kid, desc = cabi.plan(cabi.F16, layout, M, N, K, align=align)
