@@ -237,6 +237,39 @@ def test_skinny_linear_weight_binding_and_c_abi(dtype):
     assert torch.equal(out, c)
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_weight_layout_batched_and_bias_c_abi(dtype):
+    """[N, K] B through the C ABI: a batch of decode-shaped products (skinny_nk, one
+    launch over grid.z) equal per entry to the single products, and a short-K product
+    with many columns and a column bias (tile64x256), both against the oracle."""
+    g = torch.Generator().manual_seed(11)
+    Bn, M, N, K = 3, 16, 1000, 520
+    a = (torch.randn(Bn, M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    w = (torch.randn(Bn, N, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    assert "skinny_nk" in cmpext3.plan(dtype, M, N, K, layout="NK", batch=Bn)
+    ag, wg = a.cuda(), w.cuda()
+    c = torch.empty(Bn, M, N, dtype=DT[dtype], device="cuda")
+    st = cabi.gemm_ex(CODE[dtype], cabi.B_NK, ag, K, M * K, wg, K, N * K, c, N, M * N, None, M, N, K, Bn)
+    assert st == cabi.OK
+    for i in range(Bn):
+        ci = torch.empty(M, N, dtype=DT[dtype], device="cuda")
+        assert cabi.gemm_ex(CODE[dtype], cabi.B_NK, ag[i], K, 0, wg[i], K, 0, ci, N, 0, None, M, N, K) == cabi.OK
+        torch.cuda.synchronize()
+        assert torch.equal(ci, c[i])
+        ref = O.linear_f64(O.to_f64(a[i]), O.to_f64(w[i]))
+        assert O.rel_frobenius(O.to_f64(c[i].cpu()), ref) <= O.TOLERANCE[dtype]
+    M, N, K = 48, 65536 + 40, 200
+    x = (torch.randn(M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    w2 = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    bias = torch.randn(N, generator=g).to(DT[dtype])
+    assert "tile64x256" in cmpext3.plan(dtype, M, N, K, layout="NK", has_bias=True)
+    SEEN_KERNELS.add("tile64x256")
+    out = cmpext3.linear(x.cuda(), w2.cuda(), bias.cuda())
+    torch.cuda.synchronize()
+    ref = O.linear_f64(O.to_f64(x), O.to_f64(w2), O.to_f64(bias))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+
+
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
 def test_views_and_layouts(dtype):
     g = torch.Generator().manual_seed(9)
