@@ -75,6 +75,9 @@ int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride
   r.stride_b = stride_b;
   r.stride_c = stride_c;
   r.align = std::min(std::min(align_of(A), align_of(B)), std::min(align_of(C), align_of(bias)));
+  r.align_a = align_of(A);
+  r.align_b = align_of(B);
+  r.align_c = std::min(align_of(C), align_of(bias));
   r.has_bias = bias != nullptr;
   r.batch = batch;
   r.ws_bytes = (workspace != nullptr && align_of(workspace) >= 16) ? workspace_bytes : 0;
@@ -85,6 +88,34 @@ int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride
   if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return CMPEXT3_ERR_INVALID_ARG;
 
   const int64_t esz = dtype == kF32 ? 4 : 2;
+  hipStream_t s = (hipStream_t)stream;
+  // zero-padded aligned copies of unaligned 16-bit operands (planned by make_plan)
+  char* ws = (char*)workspace;
+  const bool kn = b_layout == CMPEXT3_B_KN;
+  if (plan.pad_a) {
+    const int64_t copies = (batch > 1 && stride_a != 0) ? batch : 1;
+    const hipError_t e = launch_pad_copy(A, lda, stride_a, M, K, ws, plan.lda_p, plan.stride_a_p, M, (int)plan.kp,
+                                         copies, s);
+    if (e != hipSuccess) return (int)e;
+    A = ws;
+    lda = plan.lda_p;
+    stride_a = plan.stride_a_p;
+    ws += plan.pad_a_bytes;
+  }
+  if (plan.pad_b) {
+    const int64_t copies = (batch > 1 && stride_b != 0) ? batch : 1;
+    const int rows = kn ? K : N, cols = kn ? N : K;
+    const int dst_rows = kn ? (int)plan.kp : N;
+    const hipError_t e = launch_pad_copy(B, ldb, stride_b, rows, cols, ws, plan.ldb_p, plan.stride_b_p, dst_rows,
+                                         (int)plan.ldb_p, copies, s);
+    if (e != hipSuccess) return (int)e;
+    B = ws;
+    ldb = plan.ldb_p;
+    stride_b = plan.stride_b_p;
+    ws += plan.pad_b_bytes;
+  }
+  if (plan.pad_a || plan.pad_b) K = (int)plan.kp;
+  workspace = ws;
   GemmParams p{};
   p.bias = bias;
   p.bias_row = bias_row;
@@ -100,7 +131,6 @@ int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride
   p.tiles_m = plan.tiles_m;
   p.tiles_n = plan.tiles_n;
   p.group_m = plan.group_m;
-  hipStream_t s = (hipStream_t)stream;
   for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridZ) {
     const int64_t nb = std::min<int64_t>(kMaxGridZ, batch - b0);
     p.A = (const char*)A + b0 * stride_a * esz;

@@ -81,7 +81,8 @@ const char* kernel_name(KernelId id) {
 
 }  // namespace
 
-int make_plan(const Request& r, Plan* plan) {
+namespace {
+int make_plan_core(const Request& r, Plan* plan) {
   if (r.dtype != kF16 && r.dtype != kBF16 && r.dtype != kF32) return CMPEXT3_ERR_UNSUPPORTED;
   if (r.layout != kKN && r.layout != kNK) return CMPEXT3_ERR_UNSUPPORTED;
   if (r.M < 0 || r.N < 0 || r.K < 0 || r.batch < 0) return CMPEXT3_ERR_INVALID_ARG;
@@ -111,9 +112,10 @@ int make_plan(const Request& r, Plan* plan) {
     const bool skinny_ok = r.M <= 64 && r.align >= 16 && r.K % 8 == 0 &&
                            r.lda % 8 == 0 && r.N % 8 == 0 && r.ldb % 8 == 0 &&
                            (!batched || (r.stride_a % 8 == 0 && r.stride_b % 8 == 0));
+    // (the tiled kernels' epilogue stores in 16-, 8- or 2-byte pieces as C's rows allow)
     const bool fast = r.align >= 16 && r.K % 8 == 0 && r.lda % 8 == 0 && r.ldb % 8 == 0 &&
-                      r.ldc % 4 == 0 && (r.layout == kNK || r.N % 8 == 0) &&
-                      (!batched || (r.stride_a % 8 == 0 && r.stride_b % 8 == 0 && r.stride_c % 4 == 0));
+                      (r.layout == kNK || r.N % 8 == 0 || r.b_cols_padded) &&
+                      (!batched || (r.stride_a % 8 == 0 && r.stride_b % 8 == 0));
     // With M <= 64 the skinny kernels pay off only where the GPU would otherwise
     // starve: once 128-column tiles alone give every CU one (N >= 32768, or a
     // batch of such products, e.g. a 1x1 convolution over many pixels), the tiled
@@ -185,6 +187,61 @@ int make_plan(const Request& r, Plan* plan) {
   *plan = p;
   return CMPEXT3_OK;
 }
+}  // namespace
+
+// Plans the request; when the only kernel that fits a 16-bit product is the
+// element-wise generic one (rows not 16-byte aligned), and the product is large
+// enough to pay for two copies, plans zero-padded, aligned copies of A and/or B in
+// the workspace instead (K padded to a multiple of 8 with zeros, which adds
+// exact zeros to every sum) and a tiled kernel on them.
+int make_plan(const Request& r, Plan* plan) {
+  const int st = make_plan_core(r, plan);
+  if (st != CMPEXT3_OK || plan->kernel != kGeneric16) return st;
+  const double work = (double)r.M * (double)r.N * (double)r.K * (double)r.batch;
+  const int aa = r.align_a ? r.align_a : r.align, ab = r.align_b ? r.align_b : r.align;
+  const int ac = r.align_c ? r.align_c : r.align;
+  if (work < (double)(1 << 24) || ac < 16) return st;
+  const bool kn = r.layout == kKN, batched = r.batch > 1;
+  const int64_t kp = cdiv(r.K, 8) * 8, np = cdiv(r.N, 8) * 8;
+  const bool pad_a = r.K % 8 != 0 || r.lda % 8 != 0 || aa < 16 || (batched && r.stride_a % 8 != 0);
+  const bool pad_b = r.K % 8 != 0 || r.ldb % 8 != 0 || ab < 16 || (kn && r.N % 8 != 0) ||
+                     (batched && r.stride_b % 8 != 0);
+  Request q = r;
+  q.K = kp;
+  int64_t a_bytes = 0, b_bytes = 0;
+  if (pad_a) {
+    q.lda = kp;
+    q.stride_a = (batched && r.stride_a != 0) ? r.M * kp : 0;
+    a_bytes = cdiv(r.M * kp * 2 * ((batched && r.stride_a != 0) ? r.batch : 1), 256) * 256;
+  }
+  if (pad_b) {
+    const int64_t rows = kn ? kp : r.N, cols = kn ? np : kp;
+    q.ldb = cols;
+    q.stride_b = (batched && r.stride_b != 0) ? rows * cols : 0;
+    q.b_cols_padded = kn;
+    b_bytes = cdiv(rows * cols * 2 * ((batched && r.stride_b != 0) ? r.batch : 1), 256) * 256;
+  }
+  if (a_bytes + b_bytes > r.ws_bytes) return st;
+  q.align_a = pad_a ? 16 : aa;
+  q.align_b = pad_b ? 16 : ab;
+  q.align = std::min(std::min(q.align_a, q.align_b), ac);
+  q.ws_bytes = r.ws_bytes - a_bytes - b_bytes;
+  Plan p2;
+  if (make_plan_core(q, &p2) != CMPEXT3_OK || p2.kernel == kGeneric16) return st;
+  p2.pad_a = pad_a;
+  p2.pad_b = pad_b;
+  p2.kp = kp;
+  p2.lda_p = q.lda;
+  p2.ldb_p = q.ldb;
+  p2.stride_a_p = q.stride_a;
+  p2.stride_b_p = q.stride_b;
+  p2.pad_a_bytes = a_bytes;
+  p2.pad_b_bytes = b_bytes;
+  p2.ws_bytes += a_bytes + b_bytes;
+  *plan = p2;
+  return CMPEXT3_OK;
+}
+
 
 std::string describe(const Request& r, const Plan& p) {
   static const char* dt[] = {"f16", "bf16", "f32"};
@@ -199,6 +256,11 @@ std::string describe(const Request& r, const Plan& p) {
   }
   if (p.kernel == kSkinnyWide) {
     snprintf(buf, sizeof buf, " splits=%d ksplit=%d workspace=%lld", p.splits, p.ksplit, (long long)p.ws_bytes);
+    s += buf;
+  }
+  if (p.pad_a || p.pad_b) {
+    snprintf(buf, sizeof buf, " padded=%s%s kp=%lld workspace=%lld", p.pad_a ? "A" : "", p.pad_b ? "B" : "",
+             (long long)p.kp, (long long)p.ws_bytes);
     s += buf;
   }
   return s;

@@ -19,7 +19,14 @@ struct Plan {
   int threads;            // workgroup size
   int splits;             // skinny wide: K splits (1 = no workspace)
   int ksplit;             // skinny wide: K range per split (multiple of 64)
-  int64_t ws_bytes;       // workspace the plan needs
+  int64_t ws_bytes;       // workspace the plan needs (padded copies first, then split-K partials)
+  // 16-bit operands whose rows are not 16-byte aligned (odd K or N, offset views)
+  // are copied, zero-padded, into the workspace so that a tiled kernel can run:
+  bool pad_a, pad_b;
+  int64_t kp;                          // the K the kernel runs with (K rounded up to 8 when padded)
+  int64_t lda_p, ldb_p;                // pitches of the copies
+  int64_t stride_a_p, stride_b_p;      // their batch strides (0: one copy shared by the batch)
+  int64_t pad_a_bytes, pad_b_bytes;    // workspace bytes of each copy (multiples of 256)
 };
 
 struct Request {
@@ -28,6 +35,8 @@ struct Request {
   int64_t lda, ldb, ldc;
   int64_t stride_a, stride_b, stride_c;
   int align;  // largest power of two (<= 16) dividing every operand address
+  int align_a, align_b, align_c;  // the same for A, B, and C with the bias (0: use `align`)
+  bool b_cols_padded;             // B ([K, N]) has zero columns up to a multiple of 8 (planner use)
   bool has_bias;
   int64_t batch;
   int64_t ws_bytes;  // workspace the caller provides (0: none)

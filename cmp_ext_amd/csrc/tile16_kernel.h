@@ -266,7 +266,9 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
   // then holds columns 16j' + 8(G/2) .. +7 of block j' = j + G%2. ----
   T* Cb = (T*)p.C + bz * p.stride_c;
   const uint16_t* bias = (const uint16_t*)p.bias;
-  const bool st16 = (p.ldc & 7) == 0;
+  // store width C's rows allow (every batch entry's): 16 bytes, 8 bytes, or one element
+  const int64_t cpitch = p.ldc | (gridDim.z > 1 ? p.stride_c : 0);
+  const bool st16 = (cpitch & 7) == 0, st8 = (cpitch & 3) == 0;
   const int mw = m0 + wm * S::WTM, nw = n0 + wn * S::WTN;
   auto bias_add = [&](int i, int j, f32x4 v) {
     if constexpr (BIAS == 2) {
@@ -317,7 +319,7 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
           const u32x4 v = {P0[0], P0[1], P1[0], P1[1]};
           if (n + 8 <= N && st16) {
             *(u32x4*)dst = v;
-          } else if (n + 8 <= N) {  // ldc % 8 == 4: 8-byte aligned rows
+          } else if (n + 8 <= N && st8) {  // 8-byte aligned rows
             *(u32x2*)dst = u32x2{v.x, v.y};
             *(u32x2*)(dst + 4) = u32x2{v.z, v.w};
           } else {
@@ -331,7 +333,7 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
         if (m < M && n < N) {
           T* dst = Cb + (int64_t)m * p.ldc + n;
           const u32x2 v = {P0[0], P0[1]};
-          if (n + 4 <= N) {
+          if (n + 4 <= N && st8) {
             *(u32x2*)dst = v;
           } else {
 #pragma unroll

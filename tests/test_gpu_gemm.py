@@ -270,6 +270,48 @@ def test_weight_layout_batched_and_bias_c_abi(dtype):
     assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_unaligned_operands_padded(dtype):
+    """16-bit operands whose rows are not 16-byte aligned (odd K, odd N, offset views):
+    the bindings pass a workspace, so A and/or B are copied zero-padded and a tiled
+    kernel runs; the C ABI without a workspace runs the generic kernel.  Both against
+    the oracle; C's odd row pitch is written element by element."""
+    g = torch.Generator().manual_seed(21)
+    for M, N, K in [(1023, 1025, 1027), (1024, 1031, 1024), (640, 1024, 1001)]:
+        a = (torch.randn(M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+        b = (torch.randn(K, N, generator=g)).to(DT[dtype])
+        desc = cmpext3.plan(dtype, M, N, K)
+        assert "padded=" in desc and "generic" not in desc, desc
+        out = MATMUL[dtype](a.cuda(), b.cuda())
+        c = torch.empty(M, N, dtype=DT[dtype], device="cuda")
+        assert cabi.gemm_ex(CODE[dtype], cabi.B_KN, a.cuda(), K, 0, b.cuda(), N, 0, c, N, 0, None, M, N, K) == cabi.OK
+        torch.cuda.synchronize()
+        ref = O.matmul_f64(O.to_f64(a), O.to_f64(b))
+        assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+        assert O.rel_frobenius(O.to_f64(c.cpu()), ref) <= O.TOLERANCE[dtype]
+    # Linear with odd K and bias (W [N, K] padded), an offset view of A, a batch with odd K
+    x = (torch.randn(512, 1001, generator=g) / 32).to(DT[dtype])
+    w = (torch.randn(1999, 1001, generator=g) / 32).to(DT[dtype])
+    bias = torch.randn(1999, generator=g).to(DT[dtype])
+    out = cmpext3.linear(x.cuda(), w.cuda(), bias.cuda())
+    ref = O.linear_f64(O.to_f64(x), O.to_f64(w), O.to_f64(bias))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    base = (torch.randn(1025, 1025, generator=g) / 32).to(DT[dtype])
+    b2 = (torch.randn(1024, 768, generator=g) / 32).to(DT[dtype])
+    view = base.cuda()[1:, 1:]  # rows start 2 bytes off 16-byte alignment (generic kernel: no padded workspace)
+    out = MATMUL[dtype](view, b2.cuda())
+    ref = O.matmul_f64(O.to_f64(base[1:, 1:]), O.to_f64(b2))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    a3 = (torch.randn(3, 300, 257, generator=g) / 16).to(DT[dtype])
+    b3 = (torch.randn(3, 257, 301, generator=g) / 16).to(DT[dtype])
+    assert "padded=AB" in cmpext3.plan(dtype, 300, 301, 257, batch=3)
+    out = cmpext3.bmm(a3.cuda(), b3.cuda())
+    torch.cuda.synchronize()
+    for i in range(3):
+        ref = O.matmul_f64(O.to_f64(a3[i]), O.to_f64(b3[i]))
+        assert O.rel_frobenius(O.to_f64(out[i].cpu()), ref) <= O.TOLERANCE[dtype]
+
+
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
 def test_views_and_layouts(dtype):
     g = torch.Generator().manual_seed(9)

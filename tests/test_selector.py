@@ -58,6 +58,28 @@ def test_skinny_linear_weight_layout():
     assert kid == K_SKINNY_NK and "tile=64x32" in desc and "mb=4" in desc, desc
 
 
+def test_unaligned_16bit_operands_padded_in_the_workspace():
+    # odd K / odd N: with a workspace the planner copies A and/or B, zero-padded to
+    # 16-byte rows, and runs a tiled kernel; without one the generic kernel runs
+    for M, N, K, layout, pads in [(4095, 4095, 4095, cabi.B_KN, "AB"), (4096, 4095, 4096, cabi.B_KN, "B"),
+                                  (4096, 4096, 4095, cabi.B_NK, "AB"), (2047, 2049, 2051, cabi.B_KN, "AB")]:
+        need = cabi.workspace_size(cabi.F16, layout, M, N, K)
+        kp = (K + 7) // 8 * 8
+        a_bytes = M * kp * 2 if "A" in pads else 0
+        b_bytes = (kp * ((N + 7) // 8 * 8) if layout == cabi.B_KN else N * kp) * 2 if "B" in pads else 0
+        assert need == sum((x + 255) // 256 * 256 for x in (a_bytes, b_bytes)), (M, N, K, need)
+        kid, desc = cabi.plan(cabi.F16, layout, M, N, K, workspace_bytes=need)
+        assert kid in (K_TILE256, K_TILE224, K_TILE128) and f"padded={pads} kp={kp}" in desc, desc
+        kid, desc = cabi.plan(cabi.F16, layout, M, N, K, workspace_bytes=need - 1)
+        assert kid == K_GENERIC, desc
+    # a misaligned view (offset by one element) is copied even when the shape is aligned
+    kid, desc = cabi.plan(cabi.BF16, cabi.B_KN, 2048, 2048, 2048, lda=2049, workspace_bytes=1 << 30)
+    assert kid != K_GENERIC and "padded=A " in desc, desc
+    # small products stay on the generic kernel (two copies would cost more than they save)
+    kid, _ = cabi.plan(cabi.F16, cabi.B_KN, 129, 257, 65, workspace_bytes=1 << 30)
+    assert kid == K_GENERIC
+
+
 def test_skinny_parameters():
     kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 16, 8192, 8192)
     assert kid == K_SKINNY
@@ -69,7 +91,7 @@ def test_skinny_parameters():
 @pytest.mark.parametrize("M,N,K,layout,align,expect", [
     (300, 7, 64, cabi.B_KN, 16, K_GENERIC),     # N % 8 != 0 with KN layout
     (300, 12, 64, cabi.B_NK, 16, K_TILE128),    # NK layout needs only N % 4 (8-byte C rows)
-    (300, 7, 64, cabi.B_NK, 16, K_GENERIC),     # ... which N = 7 is not
+    (300, 7, 64, cabi.B_NK, 16, K_TILE128),     # any C pitch: stores narrow to 8 or 2 bytes
     (300, 64, 33, cabi.B_KN, 16, K_GENERIC),    # K % 8 != 0
     (300, 64, 64, cabi.B_KN, 8, K_GENERIC),     # misaligned operand
     (16, 63, 64, cabi.B_KN, 16, K_GENERIC),     # skinny needs N % 8 == 0
