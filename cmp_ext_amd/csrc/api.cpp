@@ -34,9 +34,20 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
         e = launch_skinny_reduce((DType)dtype, p, (const float*)ws, plan.splits, (int)grid.z, s);
       return e;
     }
+    case kTile128x128:
+      if (plan.splits > 1) {  // split K: fp32 partials, then the reduction adds the bias and rounds
+        GemmParams q = p;
+        q.splits = plan.splits;
+        q.ksplit = plan.ksplit;
+        q.partials = (float*)ws;
+        const dim3 g(grid.x, grid.y, grid.z * plan.splits);
+        hipError_t e = dtype == kF16 ? launch_tile_f16(plan.kernel, lay, q, g, s) : launch_tile_bf16(plan.kernel, lay, q, g, s);
+        if (e == hipSuccess) e = launch_skinny_reduce((DType)dtype, p, (const float*)ws, plan.splits, (int)grid.z, s);
+        return e;
+      }
+      [[fallthrough]];
     case kTile256x256:
     case kTile256x224:
-    case kTile128x128:
     case kTile64x256:
       return dtype == kF16 ? launch_tile_f16(plan.kernel, lay, p, grid, s)
                            : launch_tile_bf16(plan.kernel, lay, p, grid, s);
@@ -131,8 +142,9 @@ int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride
   p.tiles_m = plan.tiles_m;
   p.tiles_n = plan.tiles_n;
   p.group_m = plan.group_m;
-  for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridZ) {
-    const int64_t nb = std::min<int64_t>(kMaxGridZ, batch - b0);
+  const int64_t zmax = kMaxGridZ / std::max(1, plan.kernel == kTile128x128 ? plan.splits : 1);
+  for (int64_t b0 = 0; b0 < batch; b0 += zmax) {
+    const int64_t nb = std::min<int64_t>(zmax, batch - b0);
     p.A = (const char*)A + b0 * stride_a * esz;
     p.B = (const char*)B + b0 * stride_b * esz;
     p.C = (char*)C + b0 * stride_c * esz;

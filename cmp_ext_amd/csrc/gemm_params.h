@@ -22,6 +22,10 @@ struct GemmParams {
   int M, N, K;
   int tiles_m, tiles_n;  // grid of output tiles (tiled kernels)
   int group_m;           // rows of tiles per ordering group
+  // split-K tiled products: grid.z = batch * splits, split s sums k in [s*ksplit, (s+1)*ksplit)
+  // and writes fp32 partials[s][batch][M][N] (summed, biased and rounded by a second launch)
+  int splits, ksplit;
+  float* partials;
 };
 
 // Every kernel the library can launch.  The selector returns one of these.

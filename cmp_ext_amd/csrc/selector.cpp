@@ -170,6 +170,23 @@ int make_plan_core(const Request& r, Plan* plan) {
       p.bm = c->bm;
       p.bn = c->bn;
       if (c->id != kTile128x128) p.threads = 512;  // the 256-row tiles run 8 waves, 128x128 4
+      // Few tiles and a long K (e.g. 256 x 4096 x 14336: 64 tiles of 128x128 for 512
+      // workgroup slots): split K over 128x128 tiles until ~2 workgroups per CU exist,
+      // fp32 partials in the workspace, summed by a second launch.
+      const int64_t t128 = cdiv(r.M, 128) * cdiv(r.N, 128) * r.batch;
+      // (each split keeps >= 8 K steps so that its partial block is worth writing)
+      if (r.N % 4 == 0 && 4 * t128 <= 2 * kNumCUs && r.K >= 2048) {
+        const int64_t splits = std::min<int64_t>({16, std::max<int64_t>(2, 2 * kNumCUs / t128), r.K / 512});
+        const int64_t need = splits * r.batch * r.M * r.N * 4;
+        if (splits >= 2 && need <= r.ws_bytes) {
+          p.kernel = kTile128x128;
+          p.bm = p.bn = 128;
+          p.threads = 256;
+          p.splits = (int)splits;
+          p.ksplit = (int)(cdiv(cdiv(r.K, splits), 64) * 64);
+          p.ws_bytes = need;
+        }
+      }
     } else {
       p.kernel = kGeneric16;
       p.bm = 64;
@@ -254,7 +271,7 @@ std::string describe(const Request& r, const Plan& p) {
     snprintf(buf, sizeof buf, " mb=%d", p.mb);
     s += buf;
   }
-  if (p.kernel == kSkinnyWide) {
+  if (p.kernel == kSkinnyWide || (p.kernel == kTile128x128 && p.splits > 1)) {
     snprintf(buf, sizeof buf, " splits=%d ksplit=%d workspace=%lld", p.splits, p.ksplit, (long long)p.ws_bytes);
     s += buf;
   }

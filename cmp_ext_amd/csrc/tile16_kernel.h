@@ -100,7 +100,9 @@ struct Tile16Shape {
 // BIAS: 0 none, 1 per column of C (Linear), 2 per row (conv 1x1).  A kernel per
 // mode keeps the bias-free epilogue lean: the register allocator then keeps the
 // accumulators in AGPRs through the main loop.
-template <typename T, bool KN, int BM, int BN, int WM, int WN, int BIAS, int MINB>
+// SPLITK: grid.z = batch * p.splits; this workgroup sums its split's K range and
+// stores the fp32 sums (no bias, no rounding) into p.partials.
+template <typename T, bool KN, int BM, int BN, int WM, int WN, int BIAS, int MINB, bool SPLITK = false>
 __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const GemmParams p) {
   using S = Tile16Shape<BM, BN, KN, WM, WN>;
   constexpr int FM = S::FM, FN = S::FN;
@@ -115,11 +117,16 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
   int bzi;
   tile_coords(blockIdx.x, blockIdx.z, gridDim.z, p.tiles_m, p.tiles_n, p.group_m, tm, tn, bzi);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int M = p.M, N = p.N, K = p.K;
+  const int M = p.M, N = p.N;
   const int64_t lda = p.lda, ldb = p.ldb;
-  const int64_t bz = bzi;
-  const T* Abase = (const T*)p.A + bz * p.stride_a + (int64_t)m0 * lda;
-  const T* Bbase = KN ? (const T*)p.B + bz * p.stride_b + n0 : (const T*)p.B + bz * p.stride_b + (int64_t)n0 * ldb;
+  // split-K: entry bzi of the grid's z range is split bzi % splits of batch entry bzi / splits
+  const int ks = SPLITK ? bzi % p.splits : 0;
+  const int64_t bz = SPLITK ? bzi / p.splits : bzi;
+  const int kbeg = SPLITK ? ks * p.ksplit : 0;
+  const int K = SPLITK ? min(p.K - kbeg, p.ksplit) : p.K;  // this workgroup's K range
+  const T* Abase = (const T*)p.A + bz * p.stride_a + (int64_t)m0 * lda + kbeg;
+  const T* Bbase = KN ? (const T*)p.B + bz * p.stride_b + (int64_t)kbeg * ldb + n0
+                      : (const T*)p.B + bz * p.stride_b + (int64_t)n0 * ldb + kbeg;
 
   // ---- per-lane DMA sources, relative to the step's first k; rows past the matrix are OOB ----
   uint32_t a_off[S::A_DMA];
@@ -264,6 +271,19 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
   // For a pair of blocks (j, j+1), one v_permlane16_swap per dword trades G = 1's columns
   // of block j for G = 0's of block j+1 (and G = 3's of j for G = 2's of j+1): lane (r16, G)
   // then holds columns 16j' + 8(G/2) .. +7 of block j' = j + G%2. ----
+  if constexpr (SPLITK) {
+    // fp32 partial sums: acc[i][j] holds C[16i + r16][16j + 4G .. +3] of the wave's block
+    // (N % 4 == 0, so the four columns are all in or all out)
+    const int batch = (int)gridDim.z / p.splits;
+    float* part = p.partials + ((int64_t)ks * batch + bz) * M * N;
+    const int mw = m0 + wm * S::WTM, nw = n0 + wn * S::WTN;
+    static_for<FM * FN>([&](auto xc) {
+      constexpr int x = decltype(xc)::value;
+      const int m = mw + 16 * (x / FN) + r16, n = nw + 16 * (x % FN) + 4 * G;
+      if (m < M && n < N) *(f32x4*)(part + (int64_t)m * N + n) = acc[x / FN][x % FN];
+    });
+    return;
+  }
   T* Cb = (T*)p.C + bz * p.stride_c;
   const uint16_t* bias = (const uint16_t*)p.bias;
   // store width C's rows allow (every batch entry's): 16 bytes, 8 bytes, or one element
@@ -351,6 +371,12 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
 template <typename T, bool KN, int BM, int BN, int WM, int WN, int MINB>
 void launch_tile16(const GemmParams& p, dim3 grid, hipStream_t s) {
   const dim3 block(64 * WM * WN);
+  if constexpr (BM == 128 && BN == 128) {
+    if (p.splits > 1) {  // fp32 partials; the bias comes with the reduction
+      hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 0, MINB, true>), grid, block, 0, s, p);
+      return;
+    }
+  }
   if (p.bias == nullptr)
     hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 0, MINB>), grid, block, 0, s, p);
   else if (p.bias_row)

@@ -78,6 +78,8 @@ def test_generic_ragged(dtype, M, N, K):
     (1000, 1000, 776, "tile128x128"),    # ragged, K not a multiple of 64
     (64, 32768, 128, "tile128x128"),     # M <= 64 with 256 column tiles
     (16, 32768, 264, "tile128x128"),
+    (256, 4096, 4096, "tile128x128"),    # few tiles, long K: split K (fp32 partials + reduce)
+    (200, 1000, 3000, "tile128x128"),    # ... ragged, last split shorter
     (64, 65536, 512, "tile64x256"),      # M <= 64, short K, 256 tiles of 256 columns
     (40, 70000, 200, "tile64x256"),      # ragged rows, columns and K
     (4000, 4088, 1000, "tile256x256"),   # ragged 256x256 tiles

@@ -80,6 +80,21 @@ def test_unaligned_16bit_operands_padded_in_the_workspace():
     assert kid == K_GENERIC
 
 
+def test_split_k_tiles():
+    need = cabi.workspace_size(cabi.F16, cabi.B_KN, 256, 4096, 14336)
+    assert need == 8 * 256 * 4096 * 4
+    kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 256, 4096, 14336, workspace_bytes=need)
+    assert kid == K_TILE128 and "splits=8 ksplit=1792" in desc, desc
+    kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 256, 4096, 14336)      # no workspace: one pass
+    assert kid != K_TILE128 or "splits" not in desc, desc
+    kid, desc = cabi.plan(cabi.BF16, cabi.B_NK, 200, 1000, 3000, has_bias=True, workspace_bytes=1 << 30)
+    assert kid == K_TILE128 and "splits=5 ksplit=640" in desc, desc
+    kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 1024, 1024, 1024, workspace_bytes=1 << 30)
+    assert "splits" not in desc, desc                              # short K: no split
+    kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 4096, 4096, 4096, workspace_bytes=1 << 30)
+    assert kid == K_TILE256, desc                                  # enough tiles: no split
+
+
 def test_skinny_parameters():
     kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 16, 8192, 8192)
     assert kid == K_SKINNY
