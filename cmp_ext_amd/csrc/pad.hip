@@ -10,34 +10,42 @@
 
 namespace cmpext3 {
 namespace {
-// 256 threads copy 2048 consecutive elements of the (dense) dst block: element
-// loads with consecutive lanes on consecutive elements, regrouped through LDS so
-// that each thread then writes 8 of them with one 16-byte store.
+// 256 threads copy kChunk consecutive elements of the (dense) dst block: element
+// loads with consecutive lanes on consecutive elements (32 per thread in flight),
+// regrouped through LDS so that each thread then writes 8 of them per 16-byte store.
+constexpr int kPer = 32, kChunk = 256 * kPer;
 __global__ void __launch_bounds__(256) pad_copy_kernel(const uint16_t* __restrict__ src, int64_t src_ld,
                                                        int64_t src_stride, int rows, int cols,
                                                        uint16_t* __restrict__ dst, int64_t dst_stride,
                                                        int dst_rows, int dst_cols) {
-  __shared__ __attribute__((aligned(16))) uint16_t buf[2048];
+  __shared__ __attribute__((aligned(16))) uint16_t buf[kChunk];
   const int64_t total = (int64_t)dst_rows * dst_cols;
-  const int64_t e0 = (int64_t)blockIdx.x * 2048;
+  const int64_t e0 = (int64_t)blockIdx.x * kChunk;
   const int64_t b = blockIdx.z;
   const uint16_t* s = src + b * src_stride;
   const int tid = threadIdx.x;
   int r = (int)((e0 + tid) / dst_cols);
   int c = (int)((e0 + tid) - (int64_t)r * dst_cols);
+  uint16_t v[kPer];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {  // element e0 + tid + 256 i: advance (r, c) by 256
+  for (int i = 0; i < kPer; ++i) {  // element e0 + tid + 256 i: advance (r, c) by 256
     const bool in = e0 + tid + 256 * i < total && r < rows && c < cols;
-    buf[tid + 256 * i] = in ? s[(int64_t)r * src_ld + c] : (uint16_t)0;
+    v[i] = in ? s[(int64_t)r * src_ld + c] : (uint16_t)0;
     c += 256;
     while (c >= dst_cols) {
       c -= dst_cols;
       ++r;
     }
   }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) buf[tid + 256 * i] = v[i];
   __syncthreads();
-  const int64_t e = e0 + 8 * tid;
-  if (e < total) *(u32x4*)(dst + b * dst_stride + e) = *(const u32x4*)(buf + 8 * tid);
+#pragma unroll
+  for (int j = 0; j < kPer / 8; ++j) {
+    const int q = tid + 256 * j;  // 8-element piece of the chunk
+    const int64_t e = e0 + 8 * q;
+    if (e < total) *(u32x4*)(dst + b * dst_stride + e) = *(const u32x4*)(buf + 8 * q);
+  }
 }
 }  // namespace
 
@@ -50,7 +58,7 @@ hipError_t launch_pad_copy(const void* src, int64_t src_ld, int64_t src_stride, 
   const int64_t total = (int64_t)dst_rows * dst_cols;
   for (int64_t b0 = 0; b0 < batch; b0 += kMaxZ) {
     const int64_t nb = batch - b0 < kMaxZ ? batch - b0 : kMaxZ;
-    const dim3 grid((unsigned)((total + 2047) / 2048), 1, (unsigned)nb);
+    const dim3 grid((unsigned)((total + kChunk - 1) / kChunk), 1, (unsigned)nb);
     hipLaunchKernelGGL(pad_copy_kernel, grid, block, 0, s, (const uint16_t*)src + b0 * src_stride, src_ld,
                        src_stride, rows, cols, (uint16_t*)dst + b0 * dst_stride, dst_stride, dst_rows, dst_cols);
     const hipError_t e = hipGetLastError();
