@@ -34,6 +34,8 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
         e = launch_skinny_reduce((DType)dtype, p, (const float*)ws, plan.splits, (int)grid.z, s);
       return e;
     }
+    case kTile256x256:
+    case kTile256x224:
     case kTile128x128:
       if (plan.splits > 1) {  // split K: fp32 partials, then the reduction adds the bias and rounds
         GemmParams q = p;
@@ -46,8 +48,6 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
         return e;
       }
       [[fallthrough]];
-    case kTile256x256:
-    case kTile256x224:
     case kTile64x256:
       return dtype == kF16 ? launch_tile_f16(plan.kernel, lay, p, grid, s)
                            : launch_tile_bf16(plan.kernel, lay, p, grid, s);
@@ -142,7 +142,8 @@ int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride
   p.tiles_m = plan.tiles_m;
   p.tiles_n = plan.tiles_n;
   p.group_m = plan.group_m;
-  const int64_t zmax = kMaxGridZ / std::max(1, plan.kernel == kTile128x128 ? plan.splits : 1);
+  const bool tiled = plan.kernel == kTile256x256 || plan.kernel == kTile256x224 || plan.kernel == kTile128x128;
+  const int64_t zmax = kMaxGridZ / std::max(1, tiled ? plan.splits : 1);
   for (int64_t b0 = 0; b0 < batch; b0 += zmax) {
     const int64_t nb = std::min<int64_t>(zmax, batch - b0);
     p.A = (const char*)A + b0 * stride_a * esz;

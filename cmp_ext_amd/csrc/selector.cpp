@@ -33,6 +33,19 @@ double tile_cost(const Candidate& c, int64_t M, int64_t N, int64_t batch) {
   return (double)cdiv(tiles, (int64_t)kNumCUs * c.occ) * c.occ * c.bm * c.bn / c.eff;
 }
 
+// Tiled products may split K (fp32 partials summed, biased and rounded by a second
+// launch).  Cost of a split, in the units of tile_cost: the tiles' rounds over the
+// split's K range, plus writing and reading the partials at ~5 TB/s and ~6 us for the
+// extra launch (one round of 256x256 tiles at K = 4096 takes ~102 us on MI355X).
+constexpr double kUnitsPerUs = 65536.0 * 4096.0 / 102.0;
+double split_cost(const Candidate& c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t s) {
+  const int64_t tiles = cdiv(M, c.bm) * cdiv(N, c.bn) * batch;
+  const double gemm = (double)cdiv(tiles * s, (int64_t)kNumCUs * c.occ) * c.occ * c.bm * c.bn *
+                      (double)cdiv(K, s) / c.eff;
+  const double reduce = s > 1 ? ((double)s * batch * M * N * 8.0 / 5e6 + 6.0) * kUnitsPerUs : 0.0;
+  return gemm + reduce;
+}
+
 const Candidate* pick(const Candidate* c, int n, int64_t M, int64_t N, int64_t batch) {
   const Candidate* best = &c[0];
   double best_cost = tile_cost(c[0], M, N, batch);
@@ -165,27 +178,34 @@ int make_plan_core(const Request& r, Plan* plan) {
       p.bm = 64;
       p.bn = 256;
     } else if (fast) {
-      const Candidate* c = pick(kTiles16, 3, r.M, r.N, r.batch);
-      p.kernel = c->id;
-      p.bm = c->bm;
-      p.bn = c->bn;
-      if (c->id != kTile128x128) p.threads = 512;  // the 256-row tiles run 8 waves, 128x128 4
-      // Few tiles and a long K (e.g. 256 x 4096 x 14336: 64 tiles of 128x128 for 512
-      // workgroup slots): split K over 128x128 tiles until ~2 workgroups per CU exist,
-      // fp32 partials in the workspace, summed by a second launch.
-      const int64_t t128 = cdiv(r.M, 128) * cdiv(r.N, 128) * r.batch;
-      // (each split keeps >= 8 K steps so that its partial block is worth writing)
-      if (r.N % 4 == 0 && 4 * t128 <= 2 * kNumCUs && r.K >= 2048) {
-        const int64_t splits = std::min<int64_t>({16, std::max<int64_t>(2, 2 * kNumCUs / t128), r.K / 512});
-        const int64_t need = splits * r.batch * r.M * r.N * 4;
-        if (splits >= 2 && need <= r.ws_bytes) {
-          p.kernel = kTile128x128;
-          p.bm = p.bn = 128;
-          p.threads = 256;
-          p.splits = (int)splits;
-          p.ksplit = (int)(cdiv(cdiv(r.K, splits), 64) * 64);
-          p.ws_bytes = need;
+      // Tile and K split with the lowest modelled cost.  Splitting pays where the tiles
+      // leave CUs idle and K is long (e.g. 256 x 4096 x 14336: 64 tiles of 128x128 for
+      // 512 workgroup slots); K >= 2048, each split keeps >= 8 K steps, and needs the workspace for
+      // its fp32 partials and N % 4 == 0.  Not for M <= 64: those products are bound by
+      // streaming B, which a split does not shorten.
+      const Candidate* best = &kTiles16[0];
+      int64_t best_s = 1;
+      double best_cost = -1.0;
+      for (const Candidate& c : kTiles16) {
+        const int64_t smax = (r.N % 4 == 0 && r.M > 64 && r.K >= 2048) ? std::min<int64_t>(16, r.K / 512) : 1;
+        for (int64_t s = 1; s <= std::max<int64_t>(1, smax); ++s) {
+          if (s > 1 && s * r.batch * r.M * r.N * 4 > r.ws_bytes) break;
+          const double cost = split_cost(c, r.M, r.N, r.K, r.batch, s);
+          if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            best = &c;
+            best_s = s;
+          }
         }
+      }
+      p.kernel = best->id;
+      p.bm = best->bm;
+      p.bn = best->bn;
+      if (best->id != kTile128x128) p.threads = 512;  // the 256-row tiles run 8 waves, 128x128 4
+      if (best_s > 1) {
+        p.splits = (int)best_s;
+        p.ksplit = (int)(cdiv(cdiv(r.K, best_s), 64) * 64);
+        p.ws_bytes = best_s * r.batch * r.M * r.N * 4;
       }
     } else {
       p.kernel = kGeneric16;
@@ -271,7 +291,7 @@ std::string describe(const Request& r, const Plan& p) {
     snprintf(buf, sizeof buf, " mb=%d", p.mb);
     s += buf;
   }
-  if (p.kernel == kSkinnyWide || (p.kernel == kTile128x128 && p.splits > 1)) {
+  if (p.kernel == kSkinnyWide || p.splits > 1) {
     snprintf(buf, sizeof buf, " splits=%d ksplit=%d workspace=%lld", p.splits, p.ksplit, (long long)p.ws_bytes);
     s += buf;
   }

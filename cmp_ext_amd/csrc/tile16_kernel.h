@@ -371,7 +371,7 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
 template <typename T, bool KN, int BM, int BN, int WM, int WN, int MINB>
 void launch_tile16(const GemmParams& p, dim3 grid, hipStream_t s) {
   const dim3 block(64 * WM * WN);
-  if constexpr (BM == 128 && BN == 128) {
+  if constexpr (BM >= 128) {
     if (p.splits > 1) {  // fp32 partials; the bias comes with the reduction
       hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 0, MINB, true>), grid, block, 0, s, p);
       return;

@@ -80,6 +80,8 @@ def test_generic_ragged(dtype, M, N, K):
     (16, 32768, 264, "tile128x128"),
     (256, 4096, 4096, "tile128x128"),    # few tiles, long K: split K (fp32 partials + reduce)
     (200, 1000, 3000, "tile128x128"),    # ... ragged, last split shorter
+    (512, 7168, 7168, "tile256x224"),    # 256-row tiles with K split 4 ways
+    (8192, 1024, 14336, "tile256x256"),  # ... and 2 ways
     (64, 65536, 512, "tile64x256"),      # M <= 64, short K, 256 tiles of 256 columns
     (40, 70000, 200, "tile64x256"),      # ragged rows, columns and K
     (4000, 4088, 1000, "tile256x256"),   # ragged 256x256 tiles
@@ -202,7 +204,8 @@ def test_fp16_overflow_matches_rounding():
 @pytest.mark.parametrize("shape", [(2, 150, 72, 200), (1, 4096, 4096, 4096), (3, 7, 40, 12), (1, 16, 64, 64),
                                    (1, 2048, 512, 1004), (1, 4096, 512, 3588), (2, 2048, 1024, 3588),
                                    (1, 16, 14336, 4096), (1, 1, 4096, 4096), (2, 16, 520, 1000),
-                                   (1, 64, 2048, 256)])  # the last four: decode shapes, skinny kernel on W [N,K]
+                                   (1, 64, 2048, 256),   # the four above: decode shapes, skinny kernel on W [N,K]
+                                   (1, 512, 7168, 7168)])  # split K on 256x224 tiles, bias in the reduction
 def test_linear_with_bias(dtype, shape):
     Bt, S, K, N = shape
     g = torch.Generator().manual_seed(sum(shape))
