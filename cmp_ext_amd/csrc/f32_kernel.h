@@ -59,7 +59,9 @@ __device__ __forceinline__ uint32_t f32_off(int row, int chunk) {
 // Enough resident workgroups matter more than registers here: 96 x 64 tiles at 8
 // waves per SIMD run all 2021 tiles of a 4097 x 3001 product in one round (measured
 // 460 -> 421 us on MI355X against the compiler's choice of 7).
-template <bool KN, int BM, int BN, int NS, int WAVES>
+// SPLITK: grid.z = batch * p.splits; this workgroup sums its split's K range and
+// stores the sums into p.partials (bias added by the reduction).
+template <bool KN, int BM, int BN, int NS, int WAVES, bool SPLITK = false>
 __global__ void __launch_bounds__(256, WAVES) gemm_f32_kernel(const GemmParams p) {
   using S = F32Shape<BM, BN, NS>;
   constexpr int FM = S::FM, FN = S::FN;
@@ -74,12 +76,16 @@ __global__ void __launch_bounds__(256, WAVES) gemm_f32_kernel(const GemmParams p
   int bzi;
   tile_coords(blockIdx.x, blockIdx.z, gridDim.z, p.tiles_m, p.tiles_n, p.group_m, tm, tn, bzi);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int M = p.M, N = p.N, K = p.K;
+  const int M = p.M, N = p.N;
   const int64_t lda = p.lda, ldb = p.ldb;
-  const int64_t bz = bzi;
-  const float* Abase = (const float*)p.A + bz * p.stride_a + (int64_t)m0 * lda;
-  const float* Bbase = KN ? (const float*)p.B + bz * p.stride_b + n0
-                          : (const float*)p.B + bz * p.stride_b + (int64_t)n0 * ldb;
+  // split-K: entry bzi of the grid's z range is split bzi % splits of batch entry bzi / splits
+  const int ks = SPLITK ? bzi % p.splits : 0;
+  const int64_t bz = SPLITK ? bzi / p.splits : bzi;
+  const int kbeg = SPLITK ? ks * p.ksplit : 0;
+  const int K = SPLITK ? min(p.K - kbeg, p.ksplit) : p.K;  // this workgroup's K range
+  const float* Abase = (const float*)p.A + bz * p.stride_a + (int64_t)m0 * lda + kbeg;
+  const float* Bbase = KN ? (const float*)p.B + bz * p.stride_b + (int64_t)kbeg * ldb + n0
+                          : (const float*)p.B + bz * p.stride_b + (int64_t)n0 * ldb + kbeg;
 
   // ---- DMA sources: the inverse of the LDS layouts, relative to the stage's k0 ----
   // [row][k] blocks: instruction t writes rows 4t..4t+3; lane l lands in row
@@ -189,6 +195,20 @@ __global__ void __launch_bounds__(256, WAVES) gemm_f32_kernel(const GemmParams p
   }
   asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // no LDS DMA may outlive the workgroup
 
+  if constexpr (SPLITK) {  // fp32 partial sums, four consecutive columns per store (N % 4 == 0)
+    const int batch = (int)gridDim.z / p.splits;
+    float* part = p.partials + ((int64_t)ks * batch + bz) * M * N;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = m0 + wm * S::WTM + i * 16 + r16;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn * S::WTN + j * 16 + 4 * g;
+        if (m < M && n < N) *(f32x4*)(part + (int64_t)m * N + n) = acc[i][j];
+      }
+    }
+    return;
+  }
   // acc[i][j][e] = C[m0 + wm*WTM + 16i + r16][n0 + wn*WTN + 16j + 4g + e]; elements
   // outside C get an out-of-range offset and are dropped by the store.
   const __amdgpu_buffer_rsrc_t crs = make_rsrc((float*)p.C + bz * p.stride_c + (int64_t)m0 * p.ldc + n0);

@@ -23,41 +23,25 @@ struct Candidate {
   double eff;  // relative per-flop throughput of a CU running occ of these tiles (measured)
 };
 
-// Modelled cost of running the tiles of bm x bn: tiles go out in rounds of
-// kNumCUs * occ (workgroups are handed out as slots free, and a CU's matrix
-// cores are shared by whatever it holds); a round is worth occ * bm * bn / eff
-// on the busiest CU.  Measured on MI355X this tracks the time of the fp32 and
-// 16-bit tile kernels across 512^3 .. 4096^3 and ragged shapes.
-double tile_cost(const Candidate& c, int64_t M, int64_t N, int64_t batch) {
-  const int64_t tiles = cdiv(M, c.bm) * cdiv(N, c.bn) * batch;
-  return (double)cdiv(tiles, (int64_t)kNumCUs * c.occ) * c.occ * c.bm * c.bn / c.eff;
-}
-
-// Tiled products may split K (fp32 partials summed, biased and rounded by a second
-// launch).  Cost of a split, in the units of tile_cost: the tiles' rounds over the
-// split's K range, plus writing and reading the partials at ~5 TB/s and ~6 us for the
-// extra launch (one round of 256x256 tiles at K = 4096 takes ~102 us on MI355X).
+// Modelled cost of a tiled product, optionally with K split s ways (fp32 partials
+// summed, biased and rounded by a second launch): tiles go out in rounds of
+// kNumCUs * occ (workgroups are handed out as slots free, and a CU's matrix cores
+// are shared by whatever it holds); a round is worth occ * bm * bn * (K per split) /
+// eff on the busiest CU (measured on MI355X, this tracks the fp32 and 16-bit tile
+// kernels across 512^3 .. 4096^3 and ragged shapes); a split adds writing and
+// reading the partials at ~5 TB/s and ~6 us for the extra launch.  Units per microsecond on MI355X: one round of 256x256 16-bit tiles at
+// K = 4096 takes ~102 us; fp32 4096^3 on 128x128 tiles (4 rounds) ~1040 us.
 constexpr double kUnitsPerUs = 65536.0 * 4096.0 / 102.0;
-double split_cost(const Candidate& c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t s) {
+constexpr double kUnitsPerUsF32 = 4.0 * 16384.0 * 4096.0 / 1040.0;
+double split_cost(const Candidate& c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t s,
+                  double units_per_us = kUnitsPerUs) {
   const int64_t tiles = cdiv(M, c.bm) * cdiv(N, c.bn) * batch;
   const double gemm = (double)cdiv(tiles * s, (int64_t)kNumCUs * c.occ) * c.occ * c.bm * c.bn *
                       (double)cdiv(K, s) / c.eff;
-  const double reduce = s > 1 ? ((double)s * batch * M * N * 8.0 / 5e6 + 6.0) * kUnitsPerUs : 0.0;
+  const double reduce = s > 1 ? ((double)s * batch * M * N * 8.0 / 5e6 + 6.0) * units_per_us : 0.0;
   return gemm + reduce;
 }
 
-const Candidate* pick(const Candidate* c, int n, int64_t M, int64_t N, int64_t batch) {
-  const Candidate* best = &c[0];
-  double best_cost = tile_cost(c[0], M, N, batch);
-  for (int i = 1; i < n; ++i) {
-    const double cost = tile_cost(c[i], M, N, batch);
-    if (cost < best_cost) {
-      best_cost = cost;
-      best = &c[i];
-    }
-  }
-  return best;
-}
 
 // Per-area throughput of a CU running the tile, relative to 256x256 (MI355X, fp16
 // 4096^3: 256x256 102.7 us, 128x128 with two workgroups per CU 126.7 us).
@@ -117,10 +101,31 @@ int make_plan_core(const Request& r, Plan* plan) {
   p.threads = 256;
   const bool batched = r.batch > 1;
   if (r.dtype == kF32) {
-    const Candidate* c = pick(kTiles32, 3, r.M, r.N, r.batch);
-    p.kernel = c->id;
-    p.bm = c->bm;
-    p.bn = c->bn;
+    // tile and K split with the lowest modelled cost, as for 16-bit products below (fp32
+    // has no skinny kernel, so few-tile products of any M split K; >= 16 K steps each)
+    const Candidate* best = &kTiles32[0];
+    int64_t best_s = 1;
+    double best_cost = -1.0;
+    for (const Candidate& c : kTiles32) {
+      const int64_t smax = (r.N % 4 == 0 && r.K >= 1024) ? std::min<int64_t>(16, r.K / 256) : 1;
+      for (int64_t s = 1; s <= std::max<int64_t>(1, smax); ++s) {
+        if (s > 1 && s * r.batch * r.M * r.N * 4 > r.ws_bytes) break;
+        const double cost = split_cost(c, r.M, r.N, r.K, r.batch, s, kUnitsPerUsF32);
+        if (best_cost < 0 || cost < best_cost) {
+          best_cost = cost;
+          best = &c;
+          best_s = s;
+        }
+      }
+    }
+    p.kernel = best->id;
+    p.bm = best->bm;
+    p.bn = best->bn;
+    if (best_s > 1) {
+      p.splits = (int)best_s;
+      p.ksplit = (int)(cdiv(cdiv(r.K, best_s), 64) * 64);
+      p.ws_bytes = best_s * r.batch * r.M * r.N * 4;
+    }
   } else {
     const bool skinny_ok = r.M <= 64 && r.align >= 16 && r.K % 8 == 0 &&
                            r.lda % 8 == 0 && r.N % 8 == 0 && r.ldb % 8 == 0 &&

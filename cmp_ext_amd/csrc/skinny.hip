@@ -70,7 +70,7 @@ hipError_t launch_skinny_reduce(DType dt, const GemmParams& p, const float* ws, 
   else if (dt == kBF16)
     hipLaunchKernelGGL((skinny_reduce_kernel<__bf16>), grid, dim3(256), 0, s, p, ws, splits, batch);
   else
-    return hipErrorInvalidValue;
+    hipLaunchKernelGGL((skinny_reduce_kernel<float>), grid, dim3(256), 0, s, p, ws, splits, batch);
   return hipGetLastError();
 }
 hipError_t launch_skinny_nk(DType dt, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {

@@ -17,6 +17,8 @@
 //     bias and rounds to the output type.
 #pragma once
 
+#include <type_traits>
+
 #include "device_common.h"
 
 namespace cmpext3 {
@@ -200,13 +202,20 @@ __global__ void __launch_bounds__(256) skinny_reduce_kernel(const GemmParams p, 
   const int n = (int)(rem - (int64_t)m * (N / 4)) * 4;
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
   for (int sp = 0; sp < splits; ++sp) s += *(const f32x4*)(ws + (((int64_t)sp * batch + bz) * M + m) * N + n);
-  const uint16_t* bias = (const uint16_t*)p.bias;
-  uint16_t* crow = (uint16_t*)((T*)p.C + bz * p.stride_c + (int64_t)m * p.ldc);
+  if constexpr (std::is_same<T, float>::value) {  // fp32 products (split-K fp32 tiles)
+    const float* bias = (const float*)p.bias;
+    float* crow = (float*)p.C + bz * p.stride_c + (int64_t)m * p.ldc;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    float x = s[r];
-    if (bias) x += from_bits<T>(bias[p.bias_row ? m : n + r]);
-    crow[n + r] = to_bits<T>(x);
+    for (int r = 0; r < 4; ++r) crow[n + r] = bias ? s[r] + bias[p.bias_row ? m : n + r] : s[r];
+  } else {
+    const uint16_t* bias = (const uint16_t*)p.bias;
+    uint16_t* crow = (uint16_t*)((T*)p.C + bz * p.stride_c + (int64_t)m * p.ldc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float x = s[r];
+      if (bias) x += from_bits<T>(bias[p.bias_row ? m : n + r]);
+      crow[n + r] = to_bits<T>(x);
+    }
   }
 }
 

@@ -93,7 +93,10 @@ def test_workspace_size_query():
     # decode shape: 128-column strips x 4 K splits of fp32 partials
     assert cabi.workspace_size(cabi.F16, cabi.B_KN, 16, 8192, 8192) == 4 * 16 * 8192 * 4
     assert cabi.workspace_size(cabi.F16, cabi.B_KN, 4096, 4096, 4096) == 0   # tiled kernel: none
-    assert cabi.workspace_size(cabi.F32, cabi.B_KN, 16, 8192, 8192) == 0
+    # fp32 has no skinny kernel: few tiles and a long K split K over the fp32 tiles
+    kid, desc = cabi.plan(cabi.F32, cabi.B_KN, 16, 8192, 8192, workspace_bytes=1 << 30)
+    splits = int(desc.split("splits=")[1].split()[0])
+    assert splits > 1 and cabi.workspace_size(cabi.F32, cabi.B_KN, 16, 8192, 8192) == splits * 16 * 8192 * 4
     assert cabi.workspace_size(cabi.F16, cabi.B_KN, 16, 32768, 4096) == 0    # enough strips: no split
     assert cabi.workspace_size(7, cabi.B_KN, 16, 64, 64) == cabi.ERR_UNSUPPORTED
 

@@ -317,6 +317,34 @@ def test_unaligned_operands_padded(dtype):
         assert O.rel_frobenius(O.to_f64(out[i].cpu()), ref) <= O.TOLERANCE[dtype]
 
 
+def test_fp32_split_k():
+    """fp32 products with few tiles and a long K split K over the fp32 tiles (fp32
+    partials, summed with the bias by a second launch): matmul, ragged, Linear with bias
+    and a batch, against the oracle at fp32's 1e-5."""
+    g = torch.Generator().manual_seed(31)
+    for M, N, K in [(16, 1024, 14336), (130, 1000, 4100)]:
+        assert "splits=" in cmpext3.plan("fp32", M, N, K), cmpext3.plan("fp32", M, N, K)
+        a = torch.rand(M, K, generator=g) * 2 - 1
+        b = torch.rand(K, N, generator=g) * 2 - 1
+        out = cmpext3.fp32_matmul(a.cuda(), b.cuda())
+        torch.cuda.synchronize()
+        assert err_vs_oracle(out, a, b, "fp32") <= O.TOLERANCE["fp32"]
+    x = torch.rand(64, 8192, generator=g) * 2 - 1
+    w = torch.rand(512, 8192, generator=g) * 2 - 1
+    bias = torch.rand(512, generator=g)
+    assert "splits=" in cmpext3.plan("fp32", 64, 512, 8192, layout="NK", has_bias=True)
+    out = cmpext3.linear(x.cuda(), w.cuda(), bias.cuda())
+    ref = O.linear_f64(O.to_f64(x), O.to_f64(w), O.to_f64(bias))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE["fp32"]
+    a3 = torch.rand(3, 64, 4096, generator=g) * 2 - 1
+    b3 = torch.rand(3, 4096, 256, generator=g) * 2 - 1
+    assert "splits=" in cmpext3.plan("fp32", 64, 256, 4096, batch=3)
+    out = cmpext3.bmm(a3.cuda(), b3.cuda())
+    torch.cuda.synchronize()
+    for i in range(3):
+        assert err_vs_oracle(out[i], a3[i], b3[i], "fp32") <= O.TOLERANCE["fp32"]
+
+
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
 def test_views_and_layouts(dtype):
     g = torch.Generator().manual_seed(9)
