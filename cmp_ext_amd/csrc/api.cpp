@@ -63,11 +63,11 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
         q.splits = plan.splits;
         q.ksplit = plan.ksplit;
         q.partials = (float*)ws;
-        hipError_t e = launch_f32(plan.kernel, lay, q, dim3(grid.x, grid.y, grid.z * plan.splits), s);
+        hipError_t e = launch_f32(plan.kernel, lay, plan.dma16, q, dim3(grid.x, grid.y, grid.z * plan.splits), s);
         if (e == hipSuccess) e = launch_skinny_reduce(kF32, p, (const float*)ws, plan.splits, (int)grid.z, s);
         return e;
       }
-      return launch_f32(plan.kernel, lay, p, grid, s);
+      return launch_f32(plan.kernel, lay, plan.dma16, p, grid, s);
     case kGeneric16:
       return launch_generic((DType)dtype, lay, p, grid, s);
     default:

@@ -4,28 +4,35 @@
 
 namespace cmpext3 {
 namespace {
-template <bool KN, bool SPLITK>
+template <bool KN, bool SPLITK, bool DMA16>
 hipError_t launch(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s) {
   switch (id) {
     case kF32Tile128:
-      hipLaunchKernelGGL((gemm_f32_kernel<KN, 128, 128, 2, 4, SPLITK>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((gemm_f32_kernel<KN, 128, 128, 2, 4, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
       break;
     case kF32Tile96x64:
-      hipLaunchKernelGGL((gemm_f32_kernel<KN, 96, 64, 2, 8, SPLITK>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((gemm_f32_kernel<KN, 96, 64, 2, 8, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
       break;
     case kF32Tile64:
-      hipLaunchKernelGGL((gemm_f32_kernel<KN, 64, 64, 2, 8, SPLITK>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((gemm_f32_kernel<KN, 64, 64, 2, 8, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
       break;
     default:
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
+
+template <bool DMA16>
+hipError_t launch_dma(KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s) {
+  if (p.splits > 1)
+    return lay == kKN ? launch<true, true, DMA16>(id, p, grid, s) : launch<false, true, DMA16>(id, p, grid, s);
+  return lay == kKN ? launch<true, false, DMA16>(id, p, grid, s) : launch<false, false, DMA16>(id, p, grid, s);
+}
 }  // namespace
 
-// p.splits > 1: grid.z = batch * splits, fp32 partials into p.partials.
-hipError_t launch_f32(KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s) {
-  if (p.splits > 1) return lay == kKN ? launch<true, true>(id, p, grid, s) : launch<false, true>(id, p, grid, s);
-  return lay == kKN ? launch<true, false>(id, p, grid, s) : launch<false, false>(id, p, grid, s);
+// p.splits > 1: grid.z = batch * splits, fp32 partials into p.partials.  dma16: the
+// operands meet the 16-byte LDS-DMA conditions (checked by the selector).
+hipError_t launch_f32(KernelId id, BLayout lay, bool dma16, const GemmParams& p, dim3 grid, hipStream_t s) {
+  return dma16 ? launch_dma<true>(id, lay, p, grid, s) : launch_dma<false>(id, lay, p, grid, s);
 }
 }  // namespace cmpext3

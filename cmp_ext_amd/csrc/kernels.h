@@ -16,7 +16,7 @@ hipError_t launch_skinny_wide(DType dt, int mb, const GemmParams& p, float* ws, 
                               hipStream_t s);
 hipError_t launch_skinny_reduce(DType dt, const GemmParams& p, const float* ws, int splits, int batch,
                                 hipStream_t s);
-hipError_t launch_f32(KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_f32(KernelId id, BLayout lay, bool dma16, const GemmParams& p, dim3 grid, hipStream_t s);
 hipError_t launch_generic(DType dt, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
 // dst[b][r][c] = src[b][r][c] (16-bit elements) for r < rows, c < cols, zero
 // elsewhere in dst_rows x dst_cols; dst_ld % 8 == 0 and dst 16-byte aligned.

@@ -121,6 +121,8 @@ int make_plan_core(const Request& r, Plan* plan) {
     p.kernel = best->id;
     p.bm = best->bm;
     p.bn = best->bn;
+    p.dma16 = (r.align_a ? r.align_a : r.align) >= 16 && (r.align_b ? r.align_b : r.align) >= 16 && r.K % 4 == 0 && r.lda % 4 == 0 && r.ldb % 4 == 0 &&
+              (r.layout == kNK || r.N % 4 == 0) && (!batched || (r.stride_a % 4 == 0 && r.stride_b % 4 == 0));
     if (best_s > 1) {
       p.splits = (int)best_s;
       p.ksplit = (int)(cdiv(cdiv(r.K, best_s), 64) * 64);
@@ -300,6 +302,7 @@ std::string describe(const Request& r, const Plan& p) {
     snprintf(buf, sizeof buf, " splits=%d ksplit=%d workspace=%lld", p.splits, p.ksplit, (long long)p.ws_bytes);
     s += buf;
   }
+  if (p.dma16) s += " dma16";
   if (p.pad_a || p.pad_b) {
     snprintf(buf, sizeof buf, " padded=%s%s kp=%lld workspace=%lld", p.pad_a ? "A" : "", p.pad_b ? "B" : "",
              (long long)p.kp, (long long)p.ws_bytes);

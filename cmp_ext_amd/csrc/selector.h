@@ -27,6 +27,7 @@ struct Plan {
   int64_t lda_p, ldb_p;                // pitches of the copies
   int64_t stride_a_p, stride_b_p;      // their batch strides (0: one copy shared by the batch)
   int64_t pad_a_bytes, pad_b_bytes;    // workspace bytes of each copy (multiples of 256)
+  bool dma16;  // fp32: rows 16-byte aligned, K (and N for B as [K,N]) multiples of 4
 };
 
 struct Request {

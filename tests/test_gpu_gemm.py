@@ -317,6 +317,29 @@ def test_unaligned_operands_padded(dtype):
         assert O.rel_frobenius(O.to_f64(out[i].cpu()), ref) <= O.TOLERANCE[dtype]
 
 
+@pytest.mark.parametrize("M,N,K,kernel", [(4100, 3000, 2048, "f32tile96x64"), (1000, 1000, 1028, "f32tile64x64"),
+                                          (2000, 2000, 1000, "f32tile128x128"), (200, 1000, 4100, "f32tile64x64")])
+@pytest.mark.parametrize("layout", ["KN", "NK"])
+def test_fp32_dma16(M, N, K, kernel, layout):
+    """fp32 operands with 16-byte aligned rows and K, N multiples of 4 load through
+    16-byte LDS-DMA: every tile, both B layouts, M/N tails, K % 16 != 0 and a K split."""
+    desc = cmpext3.plan("fp32", M, N, K, layout=layout)
+    assert "dma16" in desc and note_kernel("fp32", M, N, K, layout=layout) == kernel, desc
+    g = torch.Generator().manual_seed(M + K)
+    a = torch.rand(M, K, generator=g) * 2 - 1
+    b = torch.rand(K, N, generator=g) * 2 - 1 if layout == "KN" else torch.rand(N, K, generator=g) * 2 - 1
+    out = cmpext3.fp32_matmul(a.cuda(), b.cuda()) if layout == "KN" else cmpext3.linear(a.cuda(), b.cuda())
+    torch.cuda.synchronize()
+    assert err_vs_oracle(out, a, b, "fp32", layout=layout) <= O.TOLERANCE["fp32"]
+    if layout == "KN":  # a view whose rows start 4 bytes in takes the 4-byte path and agrees
+        a2 = torch.zeros(M, K + 4)
+        a2[:, 1:K + 1] = a
+        av = a2.cuda()[:, 1:K + 1]
+        out2 = cmpext3.fp32_matmul(av, b.cuda())
+        torch.cuda.synchronize()
+        assert torch.equal(out2, out)
+
+
 def test_fp32_split_k():
     """fp32 products with few tiles and a long K split K over the fp32 tiles (fp32
     partials, summed with the bias by a second launch): matmul, ragged, Linear with bias
