@@ -30,9 +30,8 @@ struct Candidate {
 // eff on the busiest CU (measured on MI355X, this tracks the fp32 and 16-bit tile
 // kernels across 512^3 .. 4096^3 and ragged shapes); a split adds writing and
 // reading the partials at ~5 TB/s and ~6 us for the extra launch.  Units per microsecond on MI355X: one round of 256x256 16-bit tiles at
-// K = 4096 takes ~102 us; fp32 4096^3 on 128x128 tiles (4 rounds) ~1040 us.
+// K = 4096 takes ~102 us.
 constexpr double kUnitsPerUs = 65536.0 * 4096.0 / 102.0;
-constexpr double kUnitsPerUsF32 = 4.0 * 16384.0 * 4096.0 / 1040.0;
 double split_cost(const Candidate& c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t s,
                   double units_per_us = kUnitsPerUs) {
   const int64_t tiles = cdiv(M, c.bm) * cdiv(N, c.bn) * batch;
@@ -50,14 +49,38 @@ const Candidate kTiles16[] = {
     {kTile256x224, 256, 224, 1, 0.98},
     {kTile128x128, 128, 128, 2, 0.81},
 };
-// fp32 4096^3 on MI355X: 128x128 131.5 TFLOP/s, 96x64 121.8, 64x64 ~117.  These
-// kernels hold 4-8 workgroups per CU whose matrix cores are shared, so a CU's
-// throughput does not depend on how many of them it holds (occ 1 in the model).
-const Candidate kTiles32[] = {
-    {kF32Tile128, 128, 128, 1, 1.00},
-    {kF32Tile96x64, 96, 64, 1, 0.926},
-    {kF32Tile64, 64, 64, 1, 0.89},
+// fp32 tiles.  A CU holds up to `occ` of their workgroups at once and shares its
+// matrix cores among them; how busy it keeps them grows with the number it holds:
+// from u1 (one workgroup, latency-bound) to umax (occ of them).  Fitted on MI355X to
+// 345 timed (tile, K split) choices over 27 shapes (M 16..4097, N 1024..4096, K
+// 1024..14336): the model's choice is within 1.7 % of the fastest measured one
+// (geometric mean; worst 1.18x at 1024^3), against 1.12x for a model with a fixed
+// per-tile efficiency.  4-byte LDS-DMA (unaligned rows) scales umax by 0.84.
+struct F32Tile {
+  KernelId id;
+  int bm, bn, occ;
+  double u1, umax;
 };
+const F32Tile kTiles32[] = {
+    {kF32Tile128, 128, 128, 4, 0.75, 0.94},
+    {kF32Tile96x64, 96, 64, 8, 0.50, 0.89},
+    {kF32Tile64, 64, 64, 8, 0.44, 0.875},
+};
+// Modelled microseconds: w = workgroups on the busiest CU, each running cdiv(K/s, 16)
+// steps of bm*bn*16 MFMA work (bm*bn*32 / (256 * 2380) us at the full fp32 rate of a
+// CU at 2.38 GHz), but no less than streaming A and B once at ~5.4 TB/s; a split
+// adds its fp32 partials written and read back at ~5.5 TB/s plus ~3.8 us.
+double f32_cost(const F32Tile& c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t s, bool dma16) {
+  const int64_t w = cdiv(cdiv(M, c.bm) * cdiv(N, c.bn) * batch * s, (int64_t)kNumCUs);
+  const double steps = (double)cdiv(cdiv(K, s), 16);
+  const double step_us = c.bm * c.bn * 32.0 / (256.0 * 2380.0);
+  const double umax = dma16 ? c.umax : 0.84 * c.umax;
+  const double u = c.u1 + (umax - c.u1) * std::min(1.0, (double)(w - 1) / (c.occ - 1));
+  const double mem = (double)batch * (M * K + K * N) * 4.0 / 5.4e6;
+  double t = 1.0 + std::max((double)w * steps * step_us / u, mem);
+  if (s > 1) t += (double)s * batch * M * N * 8.0 / 5.5e6 + 3.8;
+  return t;
+}
 
 const char* kernel_name(KernelId id) {
   switch (id) {
@@ -103,14 +126,17 @@ int make_plan_core(const Request& r, Plan* plan) {
   if (r.dtype == kF32) {
     // tile and K split with the lowest modelled cost, as for 16-bit products below (fp32
     // has no skinny kernel, so few-tile products of any M split K; >= 16 K steps each)
-    const Candidate* best = &kTiles32[0];
+    const bool dma16 = (r.align_a ? r.align_a : r.align) >= 16 && (r.align_b ? r.align_b : r.align) >= 16 &&
+                       r.K % 4 == 0 && r.lda % 4 == 0 && r.ldb % 4 == 0 && (r.layout == kNK || r.N % 4 == 0) &&
+                       (!batched || (r.stride_a % 4 == 0 && r.stride_b % 4 == 0));
+    const F32Tile* best = &kTiles32[0];
     int64_t best_s = 1;
     double best_cost = -1.0;
-    for (const Candidate& c : kTiles32) {
+    for (const F32Tile& c : kTiles32) {
       const int64_t smax = (r.N % 4 == 0 && r.K >= 1024) ? std::min<int64_t>(16, r.K / 256) : 1;
       for (int64_t s = 1; s <= std::max<int64_t>(1, smax); ++s) {
         if (s > 1 && s * r.batch * r.M * r.N * 4 > r.ws_bytes) break;
-        const double cost = split_cost(c, r.M, r.N, r.K, r.batch, s, kUnitsPerUsF32);
+        const double cost = f32_cost(c, r.M, r.N, r.K, r.batch, s, dma16);
         if (best_cost < 0 || cost < best_cost) {
           best_cost = cost;
           best = &c;
@@ -121,8 +147,7 @@ int make_plan_core(const Request& r, Plan* plan) {
     p.kernel = best->id;
     p.bm = best->bm;
     p.bn = best->bn;
-    p.dma16 = (r.align_a ? r.align_a : r.align) >= 16 && (r.align_b ? r.align_b : r.align) >= 16 && r.K % 4 == 0 && r.lda % 4 == 0 && r.ldb % 4 == 0 &&
-              (r.layout == kNK || r.N % 4 == 0) && (!batched || (r.stride_a % 4 == 0 && r.stride_b % 4 == 0));
+    p.dma16 = dma16;
     if (best_s > 1) {
       p.splits = (int)best_s;
       p.ksplit = (int)(cdiv(cdiv(r.K, best_s), 64) * 64);

@@ -317,12 +317,14 @@ def test_unaligned_operands_padded(dtype):
         assert O.rel_frobenius(O.to_f64(out[i].cpu()), ref) <= O.TOLERANCE[dtype]
 
 
-@pytest.mark.parametrize("M,N,K,kernel", [(4100, 3000, 2048, "f32tile96x64"), (1000, 1000, 1028, "f32tile64x64"),
-                                          (2000, 2000, 1000, "f32tile128x128"), (200, 1000, 4100, "f32tile64x64")])
+@pytest.mark.parametrize("M,N,K,kernel", [(4100, 3000, 2048, "f32tile96x64"), (1000, 1000, 260, "f32tile64x64"),
+                                          (2000, 2000, 1000, "f32tile128x128"), (1000, 1000, 1028, "f32tile128x128"),
+                                          (520, 516, 1028, "f32tile64x64")])
 @pytest.mark.parametrize("layout", ["KN", "NK"])
 def test_fp32_dma16(M, N, K, kernel, layout):
     """fp32 operands with 16-byte aligned rows and K, N multiples of 4 load through
-    16-byte LDS-DMA: every tile, both B layouts, M/N tails, K % 16 != 0 and a K split."""
+    16-byte LDS-DMA: every tile, both B layouts, M/N tails, K % 16 != 0 and K splits
+    (1000 x 1000 x 1028 on 128 x 128 tiles, 520 x 516 x 1028 on 64 x 64)."""
     desc = cmpext3.plan("fp32", M, N, K, layout=layout)
     assert "dma16" in desc and note_kernel("fp32", M, N, K, layout=layout) == kernel, desc
     g = torch.Generator().manual_seed(M + K)
