@@ -34,7 +34,7 @@ enum KernelId : int {
   kTile256x224 = 1,   // same, 8 waves of 64x112 (N tiles of 224)
   kTile128x128 = 2,   // same, 4 waves of 64x64, two workgroups per CU
   kSkinny = 3,        // f16/bf16, M <= 64: 32-column strips through an LDS-DMA ring
-  kF32Tile128 = 4,    // fp32 MFMA 16x16x4, 128x128 tile, 4-byte LDS-DMA ring
+  kF32Tile128 = 4,    // fp32 MFMA 16x16x4, 128x128 tile, 4- or 16-byte LDS-DMA ring
   kF32Tile64 = 5,     // same, 64x64 tile
   kGeneric16 = 6,     // f16/bf16 any shape and alignment (element loads)
   kSkinnyWide = 7,    // f16/bf16, M <= 64: 128-column strips, K split over workgroups
