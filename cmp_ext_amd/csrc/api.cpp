@@ -109,13 +109,13 @@ int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride
 
   const int64_t esz = dtype == kF32 ? 4 : 2;
   hipStream_t s = (hipStream_t)stream;
-  // zero-padded aligned copies of unaligned 16-bit operands (planned by make_plan)
+  // zero-padded aligned copies of unaligned operands (planned by make_plan)
   char* ws = (char*)workspace;
   const bool kn = b_layout == CMPEXT3_B_KN;
   if (plan.pad_a) {
     const int64_t copies = (batch > 1 && stride_a != 0) ? batch : 1;
     const hipError_t e = launch_pad_copy(A, lda, stride_a, M, K, ws, plan.lda_p, plan.stride_a_p, M, (int)plan.kp,
-                                         copies, s);
+                                         copies, (int)esz, s);
     if (e != hipSuccess) return (int)e;
     A = ws;
     lda = plan.lda_p;
@@ -127,7 +127,7 @@ int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride
     const int rows = kn ? K : N, cols = kn ? N : K;
     const int dst_rows = kn ? (int)plan.kp : N;
     const hipError_t e = launch_pad_copy(B, ldb, stride_b, rows, cols, ws, plan.ldb_p, plan.stride_b_p, dst_rows,
-                                         (int)plan.ldb_p, copies, s);
+                                         (int)plan.ldb_p, copies, (int)esz, s);
     if (e != hipSuccess) return (int)e;
     B = ws;
     ldb = plan.ldb_p;

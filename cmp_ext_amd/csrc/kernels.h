@@ -18,10 +18,11 @@ hipError_t launch_skinny_reduce(DType dt, const GemmParams& p, const float* ws, 
                                 hipStream_t s);
 hipError_t launch_f32(KernelId id, BLayout lay, bool dma16, const GemmParams& p, dim3 grid, hipStream_t s);
 hipError_t launch_generic(DType dt, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
-// dst[b][r][c] = src[b][r][c] (16-bit elements) for r < rows, c < cols, zero
-// elsewhere in dst_rows x dst_cols; dst_ld % 8 == 0 and dst 16-byte aligned.
+// dst[b][r][c] = src[b][r][c] (elements of esz = 2 or 4 bytes) for r < rows, c < cols,
+// zero elsewhere in dst_rows x dst_cols; dst_ld == dst_cols, rows of a multiple of 16
+// bytes, dst 16-byte aligned.
 hipError_t launch_pad_copy(const void* src, int64_t src_ld, int64_t src_stride, int rows, int cols, void* dst,
-                           int64_t dst_ld, int64_t dst_stride, int dst_rows, int dst_cols, int64_t batch,
+                           int64_t dst_ld, int64_t dst_stride, int dst_rows, int dst_cols, int64_t batch, int esz,
                            hipStream_t s);
 
 }  // namespace cmpext3

@@ -55,16 +55,18 @@ const Candidate kTiles16[] = {
 // 345 timed (tile, K split) choices over 27 shapes (M 16..4097, N 1024..4096, K
 // 1024..14336): the model's choice is within 1.7 % of the fastest measured one
 // (geometric mean; worst 1.18x at 1024^3), against 1.12x for a model with a fixed
-// per-tile efficiency.  4-byte LDS-DMA (unaligned rows) scales umax by 0.84.
+// per-tile efficiency.  The 4-byte LDS-DMA path (rows not 16-byte aligned) scales
+// umax by dma4, measured per tile at full occupancy against the 16-byte path on the
+// same box: 128x128 505 vs 539 us, 96x64 412 vs 423, 64x64 270 vs 321.
 struct F32Tile {
   KernelId id;
   int bm, bn, occ;
-  double u1, umax;
+  double u1, umax, dma4;
 };
 const F32Tile kTiles32[] = {
-    {kF32Tile128, 128, 128, 4, 0.75, 0.94},
-    {kF32Tile96x64, 96, 64, 8, 0.50, 0.89},
-    {kF32Tile64, 64, 64, 8, 0.44, 0.875},
+    {kF32Tile128, 128, 128, 4, 0.75, 0.94, 0.937},
+    {kF32Tile96x64, 96, 64, 8, 0.50, 0.89, 0.975},
+    {kF32Tile64, 64, 64, 8, 0.44, 0.875, 0.84},
 };
 // Modelled microseconds: w = workgroups on the busiest CU, each running cdiv(K/s, 16)
 // steps of bm*bn*16 MFMA work (bm*bn*32 / (256 * 2380) us at the full fp32 rate of a
@@ -74,7 +76,7 @@ double f32_cost(const F32Tile& c, int64_t M, int64_t N, int64_t K, int64_t batch
   const int64_t w = cdiv(cdiv(M, c.bm) * cdiv(N, c.bn) * batch * s, (int64_t)kNumCUs);
   const double steps = (double)cdiv(cdiv(K, s), 16);
   const double step_us = c.bm * c.bn * 32.0 / (256.0 * 2380.0);
-  const double umax = dma16 ? c.umax : 0.84 * c.umax;
+  const double umax = dma16 ? c.umax : c.dma4 * c.umax;
   const double u = c.u1 + (umax - c.u1) * std::min(1.0, (double)(w - 1) / (c.occ - 1));
   const double mem = (double)batch * (M * K + K * N) * 4.0 / 5.4e6;
   double t = 1.0 + std::max((double)w * steps * step_us / u, mem);
@@ -127,7 +129,8 @@ int make_plan_core(const Request& r, Plan* plan) {
     // tile and K split with the lowest modelled cost, as for 16-bit products below (fp32
     // has no skinny kernel, so few-tile products of any M split K; >= 16 K steps each)
     const bool dma16 = (r.align_a ? r.align_a : r.align) >= 16 && (r.align_b ? r.align_b : r.align) >= 16 &&
-                       r.K % 4 == 0 && r.lda % 4 == 0 && r.ldb % 4 == 0 && (r.layout == kNK || r.N % 4 == 0) &&
+                       r.K % 4 == 0 && r.lda % 4 == 0 && r.ldb % 4 == 0 &&
+                       (r.layout == kNK || r.N % 4 == 0 || r.b_cols_padded) &&
                        (!batched || (r.stride_a % 4 == 0 && r.stride_b % 4 == 0));
     const F32Tile* best = &kTiles32[0];
     int64_t best_s = 1;
@@ -263,8 +266,75 @@ int make_plan_core(const Request& r, Plan* plan) {
 // enough to pay for two copies, plans zero-padded, aligned copies of A and/or B in
 // the workspace instead (K padded to a multiple of 8 with zeros, which adds
 // exact zeros to every sum) and a tiled kernel on them.
+static const F32Tile& f32_tile(KernelId id) {
+  for (const F32Tile& c : kTiles32)
+    if (c.id == id) return c;
+  return kTiles32[0];
+}
+
+// fp32 operands whose rows are not 16-byte aligned run on the 4-byte DMA path; with a
+// workspace, zero-padded copies (K, and N for B given as [K, N], rounded up to 4) let
+// the 16-byte path run instead.  Taken when the model says the copies (read and write
+// at ~4.5 TB/s, ~4.5 us per launch) cost at least 5 % less than the 4-byte path (the
+// model is good to a few per cent here).  Measured on MI355X, padded vs direct:
+// 2500 x 2501 x 2502 310 vs 344 us, 2049 x 2999 x 3001 377 vs 410 (both padded);
+// 3001^3 492 vs 463 and cfg5 (4097 x 3001 x 2049; 96x64 loses 2.6 %) not padded.
+static int plan_f32_padded(const Request& r, Plan* plan) {
+  if (plan->dma16 || r.M == 0 || r.N == 0 || r.K == 0 || r.batch == 0) return CMPEXT3_OK;
+  const int aa = r.align_a ? r.align_a : r.align, ab = r.align_b ? r.align_b : r.align;
+  const bool kn = r.layout == kKN, batched = r.batch > 1;
+  const int64_t kp = cdiv(r.K, 4) * 4, np = cdiv(r.N, 4) * 4;
+  const bool pad_a = r.K % 4 != 0 || r.lda % 4 != 0 || aa < 16 || (batched && r.stride_a % 4 != 0);
+  const bool pad_b = r.K % 4 != 0 || r.ldb % 4 != 0 || ab < 16 || (kn && r.N % 4 != 0) ||
+                     (batched && r.stride_b % 4 != 0);
+  Request q = r;
+  q.K = kp;
+  int64_t a_bytes = 0, b_bytes = 0;
+  double copy_us = 0.0;
+  if (pad_a) {
+    const int64_t copies = (batched && r.stride_a != 0) ? r.batch : 1;
+    q.lda = kp;
+    q.stride_a = copies > 1 ? r.M * kp : 0;
+    a_bytes = cdiv(r.M * kp * 4 * copies, 256) * 256;
+    copy_us += 2.0 * (double)a_bytes / 4.5e6 + 4.5;
+  }
+  if (pad_b) {
+    const int64_t copies = (batched && r.stride_b != 0) ? r.batch : 1;
+    const int64_t rows = kn ? kp : r.N, cols = kn ? np : kp;
+    q.ldb = cols;
+    q.stride_b = copies > 1 ? rows * cols : 0;
+    q.b_cols_padded = kn;
+    b_bytes = cdiv(rows * cols * 4 * copies, 256) * 256;
+    copy_us += 2.0 * (double)b_bytes / 4.5e6 + 4.5;
+  }
+  if (a_bytes + b_bytes > r.ws_bytes) return CMPEXT3_OK;
+  q.align_a = pad_a ? 16 : aa;
+  q.align_b = pad_b ? 16 : ab;
+  q.align = std::min(q.align_a, q.align_b);
+  q.ws_bytes = r.ws_bytes - a_bytes - b_bytes;
+  Plan p2;
+  if (make_plan_core(q, &p2) != CMPEXT3_OK || !p2.dma16) return CMPEXT3_OK;
+  const double now = f32_cost(f32_tile(plan->kernel), r.M, r.N, r.K, r.batch, std::max(1, plan->splits), false);
+  const double padded =
+      copy_us + f32_cost(f32_tile(p2.kernel), r.M, r.N, kp, r.batch, std::max(1, p2.splits), true);
+  if (padded >= 0.95 * now) return CMPEXT3_OK;
+  p2.pad_a = pad_a;
+  p2.pad_b = pad_b;
+  p2.kp = kp;
+  p2.lda_p = q.lda;
+  p2.ldb_p = q.ldb;
+  p2.stride_a_p = q.stride_a;
+  p2.stride_b_p = q.stride_b;
+  p2.pad_a_bytes = a_bytes;
+  p2.pad_b_bytes = b_bytes;
+  p2.ws_bytes += a_bytes + b_bytes;
+  *plan = p2;
+  return CMPEXT3_OK;
+}
+
 int make_plan(const Request& r, Plan* plan) {
   const int st = make_plan_core(r, plan);
+  if (st == CMPEXT3_OK && r.dtype == kF32) return plan_f32_padded(r, plan);
   if (st != CMPEXT3_OK || plan->kernel != kGeneric16) return st;
   const double work = (double)r.M * (double)r.N * (double)r.K * (double)r.batch;
   const int aa = r.align_a ? r.align_a : r.align, ab = r.align_b ? r.align_b : r.align;

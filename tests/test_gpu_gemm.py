@@ -342,6 +342,44 @@ def test_fp32_dma16(M, N, K, kernel, layout):
         assert torch.equal(out2, out)
 
 
+def test_fp32_unaligned_padded():
+    """fp32 operands whose rows are not 16-byte aligned (odd K and N): with the bindings'
+    workspace, large products on the 64x64 tile copy A and B zero-padded (K and N rounded
+    up to 4) and run on the 16-byte DMA path; the C ABI without a workspace runs the
+    4-byte path on its own tile, and the two agree bit for bit: the padded K columns add
+    exact zeros in the positions the 4-byte path zero-fills, and every tile sums an
+    output's products in the same order (16-k stages, then the MFMA's fixed k order), so
+    the tile does not matter.  Linear (W as [N, K], padded) with bias, and a batch of
+    odd-K products (kept on the 4-byte path: on the 128x128 and 96x64 tiles it loses less
+    than the copies cost), against the oracle."""
+    g = torch.Generator().manual_seed(41)
+    for M, N, K in [(2049, 2999, 3001), (2500, 2501, 2502)]:
+        desc = cmpext3.plan("fp32", M, N, K)
+        assert "padded=AB" in desc and "dma16" in desc, desc
+        assert "padded" not in cabi.plan(cabi.F32, cabi.B_KN, M, N, K)[1]
+        a = torch.rand(M, K, generator=g) * 2 - 1
+        b = torch.rand(K, N, generator=g) * 2 - 1
+        out = cmpext3.fp32_matmul(a.cuda(), b.cuda())
+        c = torch.empty(M, N, device="cuda")
+        assert cabi.gemm_ex(cabi.F32, cabi.B_KN, a.cuda(), K, 0, b.cuda(), N, 0, c, N, 0, None, M, N, K) == cabi.OK
+        torch.cuda.synchronize()
+        assert err_vs_oracle(out, a, b, "fp32") <= O.TOLERANCE["fp32"]
+        assert torch.equal(out, c)
+    x = torch.rand(2049, 3001, generator=g) * 2 - 1
+    w = torch.rand(2999, 3001, generator=g) * 2 - 1
+    bias = torch.rand(2999, generator=g)
+    assert "padded=AB" in cmpext3.plan("fp32", 2049, 2999, 3001, layout="NK", has_bias=True)
+    out = cmpext3.linear(x.cuda(), w.cuda(), bias.cuda())
+    ref = O.linear_f64(O.to_f64(x), O.to_f64(w), O.to_f64(bias))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE["fp32"]
+    a3 = torch.rand(2, 1537, 2003, generator=g) * 2 - 1
+    b3 = torch.rand(2, 2003, 2001, generator=g) * 2 - 1
+    out = cmpext3.bmm(a3.cuda(), b3.cuda())
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert err_vs_oracle(out[i], a3[i], b3[i], "fp32") <= O.TOLERANCE["fp32"]
+
+
 def test_fp32_split_k():
     """fp32 products with few tiles and a long K split K over the fp32 tiles (fp32
     partials, summed with the bias by a second launch): matmul, ragged, Linear with bias
