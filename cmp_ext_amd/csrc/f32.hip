@@ -1,5 +1,6 @@
 // Instantiations of the fp32 MFMA GEMM.
 #include "f32_kernel.h"
+#include "f32_kwave_kernel.h"
 #include "kernels.h"
 
 namespace cmpext3 {
@@ -15,6 +16,9 @@ hipError_t launch(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s) {
       break;
     case kF32Tile64:
       hipLaunchKernelGGL((gemm_f32_kernel<KN, 64, 64, 2, 8, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
+      break;
+    case kF32Tile64K4:
+      hipLaunchKernelGGL((gemm_f32_kwave_kernel<KN, 2, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
       break;
     default:
       return hipErrorInvalidValue;

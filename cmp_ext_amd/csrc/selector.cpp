@@ -57,16 +57,21 @@ const Candidate kTiles16[] = {
 // (geometric mean; worst 1.18x at 1024^3), against 1.12x for a model with a fixed
 // per-tile efficiency.  The 4-byte LDS-DMA path (rows not 16-byte aligned) scales
 // umax by dma4, measured per tile at full occupancy against the 16-byte path on the
-// same box: 128x128 505 vs 539 us, 96x64 412 vs 423, 64x64 270 vs 321.
+// same box: 128x128 505 vs 539 us, 96x64 412 vs 423, 64x64 270 vs 321.  64x64k4 (K
+// split over the four waves, two workgroups per CU) fitted the same way to 114 more
+// timings: u1 0.62, umax 0.72; with it the model's choice is within 0.4 % of the
+// fastest measured (tile, split) over those 29 shapes.
 struct F32Tile {
   KernelId id;
   int bm, bn, occ;
   double u1, umax, dma4;
+  int kwaves;  // waves that split a workgroup's 16-k steps among them
 };
 const F32Tile kTiles32[] = {
-    {kF32Tile128, 128, 128, 4, 0.75, 0.94, 0.937},
-    {kF32Tile96x64, 96, 64, 8, 0.50, 0.89, 0.975},
-    {kF32Tile64, 64, 64, 8, 0.44, 0.875, 0.84},
+    {kF32Tile128, 128, 128, 4, 0.75, 0.94, 0.937, 1},
+    {kF32Tile96x64, 96, 64, 8, 0.50, 0.89, 0.975, 1},
+    {kF32Tile64, 64, 64, 8, 0.44, 0.875, 0.84, 1},
+    {kF32Tile64K4, 64, 64, 2, 0.62, 0.72, 0.84, 4},
 };
 // Modelled microseconds: w = workgroups on the busiest CU, each running cdiv(K/s, 16)
 // steps of bm*bn*16 MFMA work (bm*bn*32 / (256 * 2380) us at the full fp32 rate of a
@@ -74,7 +79,7 @@ const F32Tile kTiles32[] = {
 // adds its fp32 partials written and read back at ~5.5 TB/s plus ~3.8 us.
 double f32_cost(const F32Tile& c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t s, bool dma16) {
   const int64_t w = cdiv(cdiv(M, c.bm) * cdiv(N, c.bn) * batch * s, (int64_t)kNumCUs);
-  const double steps = (double)cdiv(cdiv(K, s), 16);
+  const double steps = (double)(cdiv(cdiv(cdiv(K, s), 16), c.kwaves) * c.kwaves);
   const double step_us = c.bm * c.bn * 32.0 / (256.0 * 2380.0);
   const double umax = dma16 ? c.umax : c.dma4 * c.umax;
   const double u = c.u1 + (umax - c.u1) * std::min(1.0, (double)(w - 1) / (c.occ - 1));
@@ -96,6 +101,7 @@ const char* kernel_name(KernelId id) {
     case kF32Tile128: return "f32tile128x128";
     case kF32Tile64: return "f32tile64x64";
     case kF32Tile96x64: return "f32tile96x64";
+    case kF32Tile64K4: return "f32tile64x64k4";
     case kGeneric16: return "generic64x64";
     default: return "?";
   }

@@ -4,11 +4,12 @@ import pytest
 from cmp_ext_amd import cabi
 
 K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKINNY_WIDE, K_F32_96, K_TILE64, \
-    K_SKINNY_NK = range(11)
+    K_SKINNY_NK, K_F32_64K4 = range(12)
 
 
 @pytest.mark.parametrize("dtype,M,N,K,expect", [
-    (cabi.F32, 512, 512, 512, K_F32_64),          # cfg1: 64 tiles of 64x64 beat 16 of 128x128
+    (cabi.F32, 512, 512, 512, K_F32_64K4),        # cfg1: 64 tiles of 64x64, K split over each one's waves
+    (cabi.F32, 3000, 2000, 1000, K_F32_64),       # 1504 tiles of 64x64: ~6 per CU
     (cabi.F16, 4096, 4096, 4096, K_TILE256),      # cfg2: 256 tiles = one per CU
     (cabi.BF16, 4096, 14336, 4096, K_TILE224),    # cfg3: 1024 tiles = 4 full waves
     (cabi.F16, 16, 8192, 8192, K_SKINNY),         # cfg4
