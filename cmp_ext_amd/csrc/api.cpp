@@ -59,6 +59,7 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
     case kF32Tile64:
     case kF32Tile96x64:
     case kF32Tile64K4:
+    case kF32Tile16K4:
       if (plan.splits > 1) {  // split K: fp32 partials, then the reduction adds the bias
         GemmParams q = p;
         q.splits = plan.splits;
@@ -154,7 +155,7 @@ int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride
   p.group_m = plan.group_m;
   const bool tiled = plan.kernel == kTile256x256 || plan.kernel == kTile256x224 || plan.kernel == kTile128x128 ||
                      plan.kernel == kF32Tile128 || plan.kernel == kF32Tile96x64 || plan.kernel == kF32Tile64 ||
-                     plan.kernel == kF32Tile64K4;
+                     plan.kernel == kF32Tile64K4 || plan.kernel == kF32Tile16K4;
   const int64_t zmax = kMaxGridZ / std::max(1, tiled ? plan.splits : 1);
   for (int64_t b0 = 0; b0 < batch; b0 += zmax) {
     const int64_t nb = std::min<int64_t>(zmax, batch - b0);

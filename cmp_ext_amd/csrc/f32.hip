@@ -18,7 +18,10 @@ hipError_t launch(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s) {
       hipLaunchKernelGGL((gemm_f32_kernel<KN, 64, 64, 2, 8, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
       break;
     case kF32Tile64K4:
-      hipLaunchKernelGGL((gemm_f32_kwave_kernel<KN, 2, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((gemm_f32_kwave_kernel<64, KN, 2, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
+      break;
+    case kF32Tile16K4:
+      hipLaunchKernelGGL((gemm_f32_kwave_kernel<16, KN, 2, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
       break;
     default:
       return hipErrorInvalidValue;

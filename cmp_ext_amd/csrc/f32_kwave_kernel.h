@@ -1,4 +1,5 @@
-// fp32 GEMM, 64x64 output tile with K split four ways across the workgroup's waves.
+// fp32 GEMM, 64x64 (or 16x64) output tile with K split four ways across the
+// workgroup's waves.
 //
 // For products that leave a CU only one or two workgroups (2048 x 1024 x 1024:
 // 512 tiles of 64x64, 128 of 128x128), the tiles of gemm_f32_kernel run
@@ -10,6 +11,9 @@
 // wave's own "s_waitcnt vmcnt".  At the end the four partial tiles are summed
 // through LDS in a fixed order (wave 0 + 1 + 2 + 3: deterministic), each wave
 // adding and storing 16 of the 64 rows.
+//
+// BM = 16 (16x64 tiles, four workgroups per CU) serves products with M <= 16,
+// which are bound by streaming B: the 64-row tile would compute 48 zero rows.
 //
 // Same contract, layouts and fragment order as gemm_f32_kernel (f32_kernel.h):
 // A (and B given as [N,K]) as [row][16 floats] with chunks XORed by (row/4)%4, B
@@ -25,14 +29,15 @@
 
 namespace cmpext3 {
 
-template <bool KN, int NS, bool SPLITK = false, bool DMA16 = false>
-__global__ void __launch_bounds__(256, 2) gemm_f32_kwave_kernel(const GemmParams p) {
-  constexpr int BM = 64, BN = 64, BK = 16;
-  constexpr int A_BYTES = BM * BK * 4, B_BYTES = BN * BK * 4, SUB = A_BYTES + B_BYTES;  // 8 KiB per step
+template <int BM, bool KN, int NS, bool SPLITK = false, bool DMA16 = false>
+__global__ void __launch_bounds__(256, BM == 16 ? 4 : 2) gemm_f32_kwave_kernel(const GemmParams p) {
+  static_assert(BM == 16 || BM == 64, "tile rows");
+  constexpr int BN = 64, BK = 16, FM = BM / 16;
+  constexpr int A_BYTES = BM * BK * 4, B_BYTES = BN * BK * 4, SUB = A_BYTES + B_BYTES;  // bytes per step
   constexpr int NA = DMA16 ? A_BYTES / 1024 : A_BYTES / 256;  // DMA instructions per step, all by this wave
   constexpr int NB = DMA16 ? B_BYTES / 1024 : B_BYTES / 256;
   static_assert(NS >= 2 && (NS - 2) * (NA + NB) <= 63, "ring depth / vmcnt range");
-  static_assert(4 * NS * SUB <= 80 * 1024, "two workgroups per CU");
+  static_assert(4 * NS * SUB * (BM == 16 ? 4 : 2) <= 160 * 1024, "workgroups per CU");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * NS * SUB];
 
   const int tid = threadIdx.x;
@@ -112,22 +117,22 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kwave_kernel(const GemmParams
     }
   };
 
-  // ---- fragments (lane r16 = l%16, g = l/16), the whole 64x64 tile ----
+  // ---- fragments (lane r16 = l%16, g = l/16), the whole BM x 64 tile ----
   const int r16 = lane & 15, g = lane >> 4;
   const uint32_t fa = f32_off(r16, g);                    // + 1024 per 16 rows
   const uint32_t fb_nk = A_BYTES + f32_off(r16, g);       // + 1024 per 16 columns
   const uint32_t fb_kn = A_BYTES + (uint32_t)(4 * g * BN * 4 + 4 * r16);
-  f32x4 acc[4][4];
+  f32x4 acc[FM][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto compute_step = [&](int jstep) {
     const unsigned char* stage = ring + (jstep % NS) * SUB;
-    f32x4 af[4];
+    f32x4 af[FM];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = *(const f32x4*)(stage + fa + i * 1024);
+    for (int i = 0; i < FM; ++i) af[i] = *(const f32x4*)(stage + fa + i * 1024);
     if (KN) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -135,7 +140,7 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kwave_kernel(const GemmParams
 #pragma unroll
         for (int j = 0; j < 4; ++j) bf[j] = *(const float*)(stage + fb_kn + s * BN * 4 + ((j ^ g) << 6));
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][j] = mma_f32(bf[j], af[i][s], acc[i][j]);
       }
@@ -146,7 +151,7 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kwave_kernel(const GemmParams
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
           for (int j = 0; j < 4; ++j) acc[i][j] = mma_f32(bf[j][s], af[i][s], acc[i][j]);
     }
@@ -166,44 +171,44 @@ __global__ void __launch_bounds__(256, 2) gemm_f32_kwave_kernel(const GemmParams
   }
   asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // no LDS DMA may outlive the loop
 
-  // ---- sum the four partial tiles: wave w adds rows 16w .. 16w+15 (block i = w) ----
+  // ---- sum the four partial tiles: of the FM x 4 16x16 blocks (flattened b = 4i + j),
+  // wave w adds and stores blocks FM*w .. FM*w + FM-1 (BM = 64: the 16 rows of block row
+  // w; BM = 16: column block w) ----
   __syncthreads();  // every wave is done with its ring
-  f32x4* red = (f32x4*)smem;  // [wave][i][j][lane], 16 KiB per wave
+  f32x4* red = (f32x4*)smem;  // [wave][i][j][lane], FM * 4 KiB per wave
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) red[((wave * 4 + i) * 4 + j) * 64 + lane] = acc[i][j];
+    for (int j = 0; j < 4; ++j) red[((wave * FM + i) * 4 + j) * 64 + lane] = acc[i][j];
   __syncthreads();
-  f32x4 sum[4];
+  f32x4 sum[FM];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    sum[j] = red[((0 * 4 + wave) * 4 + j) * 64 + lane];
+  for (int t = 0; t < FM; ++t) {
+    const int b = FM * wave + t;
+    sum[t] = red[b * 64 + lane];
 #pragma unroll
-    for (int q = 1; q < 4; ++q) sum[j] += red[((q * 4 + wave) * 4 + j) * 64 + lane];
+    for (int q = 1; q < 4; ++q) sum[t] += red[(q * 4 * FM + b) * 64 + lane];
   }
 
-  // sum[j][e] = C[m0 + 16*wave + r16][n0 + 16j + 4g + e]
-  const int row = 16 * wave + r16;
-  const bool row_ok = m0 + row < M;
-  if constexpr (SPLITK) {
-    const int batch = (int)gridDim.z / p.splits;
-    float* part = p.partials + ((int64_t)ks * batch + bz) * M * N;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + 16 * j + 4 * g;
-      if (row_ok && n < N) *(f32x4*)(part + (int64_t)(m0 + row) * N + n) = sum[j];
-    }
-    return;
-  }
-  const __amdgpu_buffer_rsrc_t crs = make_rsrc((float*)p.C + bz * p.stride_c + (int64_t)m0 * p.ldc + n0);
+  // sum[t][e] = C[m0 + 16i + r16][n0 + 16j + 4g + e] for block b = FM*wave + t = 4i + j
   const float* bias = p.bias_row ? nullptr : (const float*)p.bias;
   const float* rbias = p.bias_row ? (const float*)p.bias : nullptr;
-  const float bm = (rbias != nullptr && row_ok) ? rbias[m0 + row] : 0.f;
   const bool vec = ((p.ldc | N) & 3) == 0 && ((uintptr_t)((const float*)p.C + bz * p.stride_c) & 15) == 0;
+  const __amdgpu_buffer_rsrc_t crs = make_rsrc((float*)p.C + bz * p.stride_c + (int64_t)m0 * p.ldc + n0);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int col = 16 * j + 4 * g;
-    f32x4 v = sum[j];
+  for (int t = 0; t < FM; ++t) {
+    const int b = FM * wave + t;
+    const int row = 16 * (b >> 2) + r16;
+    const bool row_ok = m0 + row < M;
+    const int col = 16 * (b & 3) + 4 * g;
+    if constexpr (SPLITK) {
+      const int batch = (int)gridDim.z / p.splits;
+      float* part = p.partials + ((int64_t)ks * batch + bz) * M * N;
+      if (row_ok && n0 + col < N) *(f32x4*)(part + (int64_t)(m0 + row) * N + n0 + col) = sum[t];
+      continue;
+    }
+    const float bm = (rbias != nullptr && row_ok) ? rbias[m0 + row] : 0.f;
+    f32x4 v = sum[t];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       if (bias != nullptr) v[e] += (n0 + col + e < N) ? bias[n0 + col + e] : 0.f;

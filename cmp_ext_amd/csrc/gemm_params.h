@@ -42,7 +42,8 @@ enum KernelId : int {
   kTile64x256 = 9,    // f16/bf16 MFMA 16x16x32, 4 waves of 64x64, two workgroups per CU (M <= 64, short K)
   kSkinnyNK = 10,     // f16/bf16, M <= 64, B is [N,K]: 16- or 32-row strips of W, all of K per workgroup
   kF32Tile64K4 = 11,  // fp32, 64x64 tile, K split over the workgroup's four waves (few tiles per CU)
-  kNumKernels = 12
+  kF32Tile16K4 = 12,  // same with 16x64 tiles (M <= 16)
+  kNumKernels = 13
 };
 
 }  // namespace cmpext3

@@ -60,7 +60,10 @@ const Candidate kTiles16[] = {
 // same box: 128x128 505 vs 539 us, 96x64 412 vs 423, 64x64 270 vs 321.  64x64k4 (K
 // split over the four waves, two workgroups per CU) fitted the same way to 114 more
 // timings: u1 0.62, umax 0.72; with it the model's choice is within 0.4 % of the
-// fastest measured (tile, split) over those 29 shapes.
+// fastest measured (tile, split) over those 29 shapes.  16x64k4 (M <= 16, bound by
+// streaming B) to 134 more over 29 shapes with M <= 16: u1 0.36, umax 0.46, and a CU
+// streams its workgroups' B strips at ~19 GB/s with one of them, ~24 GB/s with more
+// (6 TB/s over 256 CUs); the choice is then within 2.7 % of the fastest measured.
 struct F32Tile {
   KernelId id;
   int bm, bn, occ;
@@ -72,10 +75,12 @@ const F32Tile kTiles32[] = {
     {kF32Tile96x64, 96, 64, 8, 0.50, 0.89, 0.975, 1},
     {kF32Tile64, 64, 64, 8, 0.44, 0.875, 0.84, 1},
     {kF32Tile64K4, 64, 64, 2, 0.62, 0.72, 0.84, 4},
+    {kF32Tile16K4, 16, 64, 4, 0.36, 0.46, 0.84, 4},
 };
 // Modelled microseconds: w = workgroups on the busiest CU, each running cdiv(K/s, 16)
 // steps of bm*bn*16 MFMA work (bm*bn*32 / (256 * 2380) us at the full fp32 rate of a
-// CU at 2.38 GHz), but no less than streaming A and B once at ~5.4 TB/s; a split
+// CU at 2.38 GHz), but no less than streaming A and B once at ~5.4 TB/s, nor than the
+// busiest CU streaming its workgroups' B strips (bn columns over their K range); a split
 // adds its fp32 partials written and read back at ~5.5 TB/s plus ~3.8 us.
 double f32_cost(const F32Tile& c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t s, bool dma16) {
   const int64_t w = cdiv(cdiv(M, c.bm) * cdiv(N, c.bn) * batch * s, (int64_t)kNumCUs);
@@ -83,7 +88,8 @@ double f32_cost(const F32Tile& c, int64_t M, int64_t N, int64_t K, int64_t batch
   const double step_us = c.bm * c.bn * 32.0 / (256.0 * 2380.0);
   const double umax = dma16 ? c.umax : c.dma4 * c.umax;
   const double u = c.u1 + (umax - c.u1) * std::min(1.0, (double)(w - 1) / (c.occ - 1));
-  const double mem = (double)batch * (M * K + K * N) * 4.0 / 5.4e6;
+  const double mem = std::max((double)batch * (M * K + K * N) * 4.0 / 5.4e6,
+                              (double)w * c.bn * cdiv(K, s) * 4.0 / (w == 1 ? 19e3 : 24e3));
   double t = 1.0 + std::max((double)w * steps * step_us / u, mem);
   if (s > 1) t += (double)s * batch * M * N * 8.0 / 5.5e6 + 3.8;
   return t;
@@ -102,6 +108,7 @@ const char* kernel_name(KernelId id) {
     case kF32Tile64: return "f32tile64x64";
     case kF32Tile96x64: return "f32tile96x64";
     case kF32Tile64K4: return "f32tile64x64k4";
+    case kF32Tile16K4: return "f32tile16x64k4";
     case kGeneric16: return "generic64x64";
     default: return "?";
   }
@@ -142,6 +149,7 @@ int make_plan_core(const Request& r, Plan* plan) {
     int64_t best_s = 1;
     double best_cost = -1.0;
     for (const F32Tile& c : kTiles32) {
+      if (c.bm == 16 && r.M > 16) continue;  // 16-row tiles: measured and meant for M <= 16 only
       const int64_t smax = (r.N % 4 == 0 && r.K >= 1024) ? std::min<int64_t>(16, r.K / 256) : 1;
       for (int64_t s = 1; s <= std::max<int64_t>(1, smax); ++s) {
         if (s > 1 && s * r.batch * r.M * r.N * 4 > r.ws_bytes) break;

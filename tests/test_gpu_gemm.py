@@ -25,7 +25,7 @@ CODE = {"fp16": cabi.F16, "bf16": cabi.BF16, "fp32": cabi.F32}
 MATMUL = {"fp16": cmpext3.fp16_matmul, "bf16": cmpext3.bf16_matmul, "fp32": cmpext3.fp32_matmul}
 KERNEL_NAMES = ["tile256x256", "tile256x224", "tile128x128", "tile64x256", "skinny", "skinny_wide", "skinny_nk",
                 "f32tile128x128",
-                "f32tile64x64", "f32tile96x64", "f32tile64x64k4", "generic64x64"]
+                "f32tile64x64", "f32tile96x64", "f32tile64x64k4", "f32tile16x64k4", "generic64x64"]
 SEEN_KERNELS = set()
 
 
@@ -379,6 +379,36 @@ def test_fp32_unaligned_padded():
     out = cmpext3.bmm(a3.cuda(), b3.cuda())
     torch.cuda.synchronize()
     for i in range(2):
+        assert err_vs_oracle(out[i], a3[i], b3[i], "fp32") <= O.TOLERANCE["fp32"]
+
+
+def test_fp32_m16_tile():
+    """fp32 products with M <= 16 run on 16x64 tiles with K split over each workgroup's
+    waves: ragged M, N and K (4-byte DMA), aligned (16-byte DMA), a K split across
+    workgroups, Linear (W as [N, K]) with bias, and a batch, against the oracle."""
+    g = torch.Generator().manual_seed(61)
+    for M, N, K in [(13, 1001, 333), (7, 3000, 777), (16, 1000, 100), (16, 4096, 4096)]:
+        assert note_kernel("fp32", M, N, K) == "f32tile16x64k4", cmpext3.plan("fp32", M, N, K)
+        a = torch.rand(M, K, generator=g) * 2 - 1
+        b = torch.rand(K, N, generator=g) * 2 - 1
+        out = cmpext3.fp32_matmul(a.cuda(), b.cuda())
+        torch.cuda.synchronize()
+        assert err_vs_oracle(out, a, b, "fp32") <= O.TOLERANCE["fp32"]
+    assert "splits=" in cmpext3.plan("fp32", 16, 4096, 4096)
+    for M, N, K in [(5, 1000, 1000), (16, 4096, 4096)]:
+        x = torch.rand(M, K, generator=g) * 2 - 1
+        w = torch.rand(N, K, generator=g) * 2 - 1
+        bias = torch.rand(N, generator=g)
+        assert note_kernel("fp32", M, N, K, layout="NK", has_bias=True) == "f32tile16x64k4"
+        out = cmpext3.linear(x.cuda(), w.cuda(), bias.cuda())
+        ref = O.linear_f64(O.to_f64(x), O.to_f64(w), O.to_f64(bias))
+        assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE["fp32"]
+    a3 = torch.rand(4, 16, 1000, generator=g) * 2 - 1
+    b3 = torch.rand(4, 1000, 512, generator=g) * 2 - 1
+    assert note_kernel("fp32", 16, 512, 1000, batch=4) == "f32tile16x64k4"
+    out = cmpext3.bmm(a3.cuda(), b3.cuda())
+    torch.cuda.synchronize()
+    for i in range(4):
         assert err_vs_oracle(out[i], a3[i], b3[i], "fp32") <= O.TOLERANCE["fp32"]
 
 
