@@ -123,8 +123,9 @@ int cmpext3_conv2d_1x1(int dtype, const void* input, const void* weight, const v
                        void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
- * Bytes of workspace cmpext3_gemm_ex can use for these arguments (packed
- * operands, 16-byte aligned); 0 when the chosen kernel needs none, or a
+ * Bytes of workspace cmpext3_gemm_ex can use for these arguments (zero-padded
+ * copies of operands whose rows are not 16-byte aligned, then split-K fp32
+ * partial sums; 16-byte aligned); 0 when the chosen kernel needs none, or a
  * negative CMPEXT3_ERR_*.  Host only.  No counterpart in the reference, whose
  * kernels never split K (one launch per product, src/main.cpp:203-227).
  */
