@@ -135,7 +135,7 @@ def rel_frobenius(out: np.ndarray, ref: np.ndarray) -> float:
 
 def make_inputs(dtype: str, M: int, N: int, K: int, dist: str, scale: float = 1.0, seed: int = 0,
                 b_layout: str = "KN"):
-    """Seeded inputs as BASELINE.md fixes them: a CPU torch.Generator seeded
+    """Seeded inputs of the benchmark configurations: a CPU torch.Generator seeded
     with `seed` draws A first, then B, both in float32 (uniform[-1, 1] or
     normal(0, 1) * scale), and each is then cast to `dtype`.  Returns torch
     CPU tensors in `dtype` (B as [K, N], or [N, K] for b_layout "NK")."""
