@@ -1,5 +1,9 @@
 // Instantiations of the skinny-M GEMM (M <= 64; B is [K, N], or [N, K] for the
 // strips-of-W kernel).
+#include <stdint.h>
+
+#include <algorithm>
+
 #include "kernels.h"
 #include "skinny_kernel.h"
 #include "skinny_wide_kernel.h"
@@ -61,16 +65,44 @@ hipError_t launch_skinny_wide(DType dt, int mb, const GemmParams& p, float* ws, 
   return hipErrorInvalidValue;
 }
 
+namespace {
+template <typename T, int V>
+void launch_reduce(const GemmParams& p, const float* ws, int splits, int batch, int vec, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((skinny_reduce_kernel<T, V>), grid, dim3(256), 0, s, p, ws, splits, batch, vec);
+}
+template <typename T>
+void launch_reduce(int V, const GemmParams& p, const float* ws, int splits, int batch, int vec, dim3 grid,
+                   hipStream_t s) {
+  if (V == 8)
+    launch_reduce<T, 8>(p, ws, splits, batch, vec, grid, s);
+  else
+    launch_reduce<T, 4>(p, ws, splits, batch, vec, grid, s);
+}
+}  // namespace
+
 hipError_t launch_skinny_reduce(DType dt, const GemmParams& p, const float* ws, int splits, int batch,
                                 hipStream_t s) {
-  const int64_t quads = (int64_t)batch * p.M * (p.N / 4);
-  const dim3 grid((unsigned)((quads + 255) / 256));
+  // The split-K kernels write partial rows of N floats with 16-byte stores, so N % 4 == 0 here.
+  if (p.N % 4 != 0 || splits < 1) return hipErrorInvalidValue;
+  const int64_t rows = (int64_t)batch * p.M;
+  if (rows <= 0 || p.N <= 0) return hipSuccess;
+  const int V = p.N % 8 == 0 ? 8 : 4;
+  const int64_t esz = dt == kF32 ? 4 : 2;
+  // C stores of V elements go out in pieces of at most 16 bytes; they need the
+  // piece size as alignment of C, of its row pitch and of its batch stride.
+  const int64_t align = std::min<int64_t>(16, V * esz);
+  const int vec = (uintptr_t)p.C % align == 0 && (p.ldc * esz) % align == 0 &&
+                  (batch == 1 || (p.stride_c * esz) % align == 0);
+  const int64_t ry = std::min<int64_t>(rows, 65535);
+  const int64_t rz = (rows + ry - 1) / ry;
+  if (rz > 65535) return hipErrorInvalidConfiguration;
+  const dim3 grid((unsigned)((p.N / V + 255) / 256), (unsigned)ry, (unsigned)rz);
   if (dt == kF16)
-    hipLaunchKernelGGL((skinny_reduce_kernel<_Float16>), grid, dim3(256), 0, s, p, ws, splits, batch);
+    launch_reduce<_Float16>(V, p, ws, splits, batch, vec, grid, s);
   else if (dt == kBF16)
-    hipLaunchKernelGGL((skinny_reduce_kernel<__bf16>), grid, dim3(256), 0, s, p, ws, splits, batch);
+    launch_reduce<__bf16>(V, p, ws, splits, batch, vec, grid, s);
   else
-    hipLaunchKernelGGL((skinny_reduce_kernel<float>), grid, dim3(256), 0, s, p, ws, splits, batch);
+    launch_reduce<float>(V, p, ws, splits, batch, vec, grid, s);
   return hipGetLastError();
 }
 hipError_t launch_skinny_nk(DType dt, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {

@@ -143,7 +143,7 @@ def test_skinny_split_k_repeated_and_concurrent():
         o2 = [cmpext3.fp16_matmul(ag, bg) for _ in range(50)]
     torch.cuda.synchronize()
     assert all(torch.equal(o, ref) for o in o1 + o2)
-    # batched: every batch entry has its own counters
+    # batched: every batch entry has its own block of partial sums
     a3 = torch.stack([ag, ag * 0.5, -ag])
     b3 = torch.stack([bg, bg, bg * 2])
     assert "splits=1 " not in cmpext3.plan("fp16", 16, 1024, 8192, batch=3)
@@ -151,6 +151,61 @@ def test_skinny_split_k_repeated_and_concurrent():
     torch.cuda.synchronize()
     for i in range(3):
         assert err_vs_oracle(o3[i], a3[i], b3[i], "fp16") <= O.TOLERANCE["fp16"]
+
+
+# Split-K reductions into every store form: N % 8 == 4 (four columns per
+# thread), C pitches and batch strides that do not keep 16-byte stores aligned
+# (element stores), per-column bias, both B layouts and all three dtypes.
+SPLIT_CASES = [
+    # dtype, layout, M, N, K, ldc, batch, stride_c, bias
+    ("fp16", "NK", 256, 1028, 8192, 1028, 1, 0, False),            # 128x128 tiles, 4 columns, 8-byte stores
+    ("bf16", "KN", 16, 1024, 8192, 1027, 1, 0, True),              # skinny_wide, odd pitch
+    ("fp16", "KN", 16, 1024, 8192, 1024, 3, 16 * 1024 + 4, False),  # batch stride off the 16-byte grid
+    ("fp16", "KN", 256, 4096, 4096, 4100, 1, 0, True),             # 128x128 tiles, pitch off the grid
+    ("bf16", "NK", 256, 2052, 4096, 2052, 1, 0, True),             # W as [N, K], 4 columns per thread
+    ("fp32", "KN", 16, 1028, 14336, 1028, 1, 0, False),            # fp32 16x64 tiles, 16-byte stores
+    ("fp32", "NK", 130, 1000, 4100, 1001, 1, 0, True),             # fp32 tiles, element stores
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "-".join(str(x) for x in c))
+def test_split_k_reduction_store_forms(case):
+    """cmpext3_gemm_ex with a workspace on products that split K: the reduction of
+    the fp32 partials writes C (plus bias) exactly where the pitches say, leaves the
+    gaps between rows and batch entries untouched, and matches the float64 oracle."""
+    dtype, layout, M, N, K, ldc, batch, stride_c, has_bias = case
+    lay = cabi.B_KN if layout == "KN" else cabi.B_NK
+    ldb = N if layout == "KN" else K
+    ws_bytes = cabi.workspace_size(CODE[dtype], lay, M, N, K, batch)
+    _, desc = cabi.plan(CODE[dtype], lay, M, N, K, ldc=ldc, has_bias=has_bias, batch=batch,
+                        workspace_bytes=ws_bytes)
+    assert "splits=" in desc and "splits=1 " not in desc, desc
+    g = torch.Generator().manual_seed(M + N + K)
+    bshape = (K, N) if layout == "KN" else (N, K)
+    a = (torch.randn(batch, M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    b = (torch.randn(batch, *bshape, generator=g) / np.sqrt(K)).to(DT[dtype])
+    bias = torch.randn(N, generator=g).to(DT[dtype]) if has_bias else None
+    stride_c = stride_c or M * ldc
+    sentinel = 7.0
+    cbuf = torch.full((stride_c * (batch - 1) + M * ldc + 8,), sentinel, dtype=DT[dtype], device="cuda")
+    ws = torch.empty(ws_bytes // 4 + 4, dtype=torch.float32, device="cuda")
+    ag, bg = a.cuda(), b.cuda()
+    st = cabi.gemm_ex(CODE[dtype], lay, ag, K, M * K, bg, ldb, K * N, cbuf, ldc, stride_c,
+                      None if bias is None else bias.cuda(), M, N, K, batch, workspace=ws)
+    assert st == cabi.OK, cabi.status_string(st)
+    torch.cuda.synchronize()
+    cpu = cbuf.cpu()
+    written = torch.zeros(cpu.numel(), dtype=torch.bool)
+    for i in range(batch):
+        rows = torch.arange(M).unsqueeze(1) * ldc + torch.arange(N).unsqueeze(0) + i * stride_c
+        written[rows.reshape(-1)] = True
+        out = cpu[rows]
+        bt = O.to_f64(b[i]) if layout == "KN" else O.to_f64(b[i]).T
+        ref = O.matmul_f64(O.to_f64(a[i]), bt)
+        if bias is not None:
+            ref = ref + O.to_f64(bias)[None, :]
+        assert O.rel_frobenius(O.to_f64(out), ref) <= O.TOLERANCE[dtype], (i, desc)
+    assert (cpu[~written] == sentinel).all(), "a store landed outside C's rows"
 
 
 @pytest.mark.parametrize("M,N,K,kernel", [(512, 512, 512, "f32tile64x64k4"), (65, 47, 3, "f32tile64x64"),
