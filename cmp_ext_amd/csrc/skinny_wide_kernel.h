@@ -31,7 +31,10 @@ struct WideShape {
   static constexpr int B_BYTES = kWideKS * kWideStrip * 2;  // 16 KB, rows of 256 bytes
   static constexpr int A_BYTES = MB * 16 * 128;             // rows of 64 k = 128 bytes
   static constexpr int STAGE = B_BYTES + A_BYTES;
-  static constexpr int NS = (160 * 1024) / STAGE > 8 ? 8 : (160 * 1024) / STAGE;
+  // Four stages (64-96 KiB): measured on MI355X against the deepest ring that fits
+  // (8, 8, 7, 6 stages for MB = 1..4), 16/32/48/64 x 8192 x 8192 with 4 splits ran
+  // 27.5/28.8/30.1/31.5 us against 28.2/29.6/30.9/31.9.
+  static constexpr int NS = 4;
   static constexpr int B_DMA = B_BYTES / 4096;  // per wave
   static constexpr int A_DMA_WG = A_BYTES / 1024;  // per workgroup, dealt round-robin to waves
   static constexpr int A_HI = (A_DMA_WG + 3) / 4;  // A loads of waves < A_DMA_WG % 4 (or all)
