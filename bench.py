@@ -16,14 +16,22 @@ HBM3E 8 TB/s).  `traffic` (HBM bytes per launch) comes from the committed
 rocprofv3 FETCH_SIZE/WRITE_SIZE summary in profiles/hbm_traffic.json when it
 has an entry for the workload, else null.
 
-cpu_baseline: the reference CPU path that BASELINE.json names -- the same op
-via torch.matmul on CPU tensors (oracle.gemm_oracle.cpu_matmul), timed on this
-host's cores over a bounded sample (about 10 s).
+cpu_baseline (every config): the reference CPU path that BASELINE.json names --
+the same op via torch.matmul on CPU tensors in the config's dtype
+(oracle.gemm_oracle.cpu_matmul), timed on this host's cores on two row samples
+of the workload (about 8 s each), both reported with their rate ratio and the
+host's CPU model, thread count and ISA.
+
+power: board power and shader clock (amdsmi gpu_metrics) read while the timed
+steps of each workload ran; MFMA-bound rooflines also carry the fraction of the
+matrix peak at that clock (`frac_at_measured_sclk`; the nominal `frac` is the
+record).  torch_same_device: the same op through torch on the same GPU, timed the
+same way, as the reference's own harness compares (context, not the measured path).
 
 callers: the three reference callers on the GEMM path, at the shapes of the
 reference's own benchmark (tools/bench.py:156-200): linear with bias, bmm and a
 1x1 conv2d, each timed like the configs, with its roofline and the same op on
-CPU tensors (torch) timed beside it over a bounded sample (about 3 s each).
+CPU tensors (torch) timed beside it on two bounded samples (about 3 s each).
 `python bench.py --caller NAME` times one of them alone (for profiling).
 """
 from __future__ import annotations
@@ -67,11 +75,176 @@ CALLERS = {
 }
 
 
+def log(msg: str) -> None:
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
 def algorithmic(c) -> tuple[float, float]:
     esz = 4 if c["dtype"] == "fp32" else 2
     flops = 2.0 * c["M"] * c["N"] * c["K"]
     nbytes = float(esz * (c["M"] * c["K"] + c["K"] * c["N"] + c["M"] * c["N"]))
     return flops, nbytes
+
+
+class PowerClock:
+    """Board power and shader clock of the GPU, read through amdsmi's gpu_metrics
+    (current_socket_power, current_gfxclks per XCD), the counterpart of the
+    reference harness's NVML power sampling (tools/bench.py:23-61).  Samples are
+    taken from the host thread while the GPU works through the already-queued
+    timed steps, so they fall inside the timed region."""
+
+    def __init__(self):
+        self.error = None
+        self.handle = None
+        try:
+            import amdsmi
+
+            self.amdsmi = amdsmi
+            amdsmi.amdsmi_init()
+            handles = amdsmi.amdsmi_get_processor_handles()
+            if not handles:
+                raise RuntimeError("no GPU handle")
+            self.handle = handles[0]
+            try:  # the handle of torch's device 0 when the bus ids can be matched
+                import torch
+
+                props = torch.cuda.get_device_properties(0)
+                bus = getattr(props, "pci_bus_id", None)
+                for h in handles:
+                    bdf = amdsmi.amdsmi_get_gpu_device_bdf(h)
+                    if bus is not None and int(bdf.split(":")[1], 16) == int(bus):
+                        self.handle = h
+                        break
+            except Exception:  # noqa: BLE001 -- keep the first handle
+                pass
+            t0 = time.perf_counter()
+            for _ in range(3):
+                self.read()
+            self.read_s = (time.perf_counter() - t0) / 3
+        except Exception as e:  # noqa: BLE001 -- power is reported as unavailable, never fatal
+            self.error = f"{type(e).__name__}: {e}"
+            self.handle = None
+
+    def read(self):
+        m = self.amdsmi.amdsmi_get_gpu_metrics_info(self.handle)
+
+        def num(x):
+            return float(x) if isinstance(x, (int, float)) else None
+
+        clks = [float(c) for c in (m.get("current_gfxclks") or []) if isinstance(c, (int, float)) and c > 0]
+        if not clks and num(m.get("current_gfxclk")):
+            clks = [num(m.get("current_gfxclk"))]
+        return {"power_w": num(m.get("current_socket_power")) or num(m.get("average_socket_power")),
+                "clks": clks, "stamp": m.get("firmware_timestamp"), "t": time.perf_counter()}
+
+    def sample_until(self, event, deadline: float, out: list) -> None:
+        """Read samples into `out` while `event` (a recorded torch event) is pending
+        and a read would end before `deadline` (perf_counter seconds), so that the
+        reads never delay the host's view of the end of the timed steps."""
+        if self.handle is None:
+            return
+        while time.perf_counter() + 1.5 * self.read_s < deadline and not event.query():
+            try:
+                out.append(self.read())
+            except Exception as e:  # noqa: BLE001
+                self.error = f"{type(e).__name__}: {e}"
+                return
+
+    def summary(self, samples: list, window_s: float = 0.0) -> dict:
+        if self.handle is None or not samples:
+            return {"samples": 0, "error": self.error or "no sample fell inside the window"}
+        # the firmware refreshes the table every few ms to seconds: keep one sample per refresh
+        # (the first sample is dropped: its table may predate the window)
+        fresh, seen = [], {samples[0]["stamp"]}
+        for x in samples[1:]:
+            if x["stamp"] not in seen:
+                seen.add(x["stamp"])
+                fresh.append(x)
+        if not fresh:
+            return {"samples": 0, "reads": len(samples),
+                    "error": "the firmware's metrics table did not refresh during the window"}
+        samples = fresh
+        pw = [x["power_w"] for x in samples if x["power_w"]]
+        clk = [sum(x["clks"]) / len(x["clks"]) for x in samples if x["clks"]]
+        lo = [min(x["clks"]) for x in samples if x["clks"]]
+        hi = [max(x["clks"]) for x in samples if x["clks"]]
+        return {"samples": len(samples),
+                "avg_power_w": round(statistics.mean(pw), 1) if pw else None,
+                "avg_sclk_mhz": round(statistics.mean(clk), 1) if clk else None,
+                "xcd_sclk_mhz_range": [round(min(lo)), round(max(hi))] if lo else None,
+                "window_s": round(window_s, 3),
+                "source": "amdsmi gpu_metrics (current_socket_power; current_gfxclks averaged over the XCDs), "
+                          "one sample per firmware refresh, read while the same op ran back to back for "
+                          "window_s right after its timed steps"}
+
+
+POWER = None
+
+
+def power_clock() -> PowerClock:
+    global POWER
+    if POWER is None:
+        POWER = PowerClock()
+    return POWER
+
+
+POWER_WINDOW_S = 1.0
+
+
+def set_power_window(seconds: float) -> None:
+    global POWER_WINDOW_S
+    POWER_WINDOW_S = seconds
+
+
+def timed_region(fn, steps: int, warmup: int, power_window_s: float | None = None) -> tuple[float, float, dict]:
+    """W untimed calls, then K calls between two events on the current stream
+    (the stream the kernels run on), bracketed by synchronizations.  Then, outside
+    the timed region, the same call back to back for `power_window_s` seconds while
+    board power and shader clock are read (the timed steps are too short for the
+    firmware's metrics to refresh inside them).  Returns (wall ms per step, event
+    ms per step, power/clock summary)."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(warmup + 1)]
+    marks[0].record(stream)
+    for i in range(warmup):
+        fn(i)
+        marks[i + 1].record(stream)
+    torch.cuda.synchronize()
+    # the GPU time of one step, from the warm-up calls (median: the first may load code)
+    est_ms = statistics.median(marks[i].elapsed_time(marks[i + 1]) for i in range(warmup)) if warmup else 0.0
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(steps):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    wall_ms, kern_ms = (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
+    window = POWER_WINDOW_S if power_window_s is None else power_window_s
+    samples = []
+    pc = power_clock()
+    if window > 0 and pc.handle is not None:
+        # batches of ~20 ms, two in flight, so the GPU never idles while the host reads
+        per = max(1, int(20.0 / max(kern_ms, 1e-3)))
+        pending = []
+        w0 = time.perf_counter()
+        i = 0
+        while time.perf_counter() - w0 < window or pending:
+            if time.perf_counter() - w0 < window:
+                for _ in range(per):
+                    fn(i)
+                    i += 1
+                ev = torch.cuda.Event()
+                ev.record(stream)
+                pending.append(ev)
+            if len(pending) >= 2 or time.perf_counter() - w0 >= window:
+                pc.sample_until(pending.pop(0), float("inf"), samples)
+        torch.cuda.synchronize()
+        window = time.perf_counter() - w0
+    return wall_ms, kern_ms, pc.summary(samples, window)
 
 
 def make_gpu_inputs(c, nb: int, seed: int = 0):
@@ -90,7 +263,7 @@ def make_gpu_inputs(c, nb: int, seed: int = 0):
     return a, bs
 
 
-def time_gpu(name: str, steps: int, warmup: int) -> dict:
+def time_gpu(name: str, steps: int, warmup: int, with_torch: bool = True) -> dict:
     import torch
 
     import cmpext3
@@ -101,25 +274,17 @@ def time_gpu(name: str, steps: int, warmup: int) -> dict:
     # Infinity Cache across calls, so it cycles through 4 distinct B buffers.
     nb = 4 if c.get("hbm") else 1
     a, bs = make_gpu_inputs(c, nb)
-    for i in range(warmup):
-        fn(a, bs[i % nb])
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for i in range(steps):
-        fn(a, bs[i % nb])
-    e1.record(stream)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    wall_ms = (t1 - t0) * 1e3 / steps
-    kern_ms = e0.elapsed_time(e1) / steps
+    wall_ms, kern_ms, pwr = timed_region(lambda i: fn(a, bs[i % nb]), steps, warmup)
+    plan = cmpext3.last_plan()
     flops, nbytes = algorithmic(c)
-    r = dict(config=name, desc=c["desc"], dtype=c["dtype"], kernel=cmpext3.plan(c["dtype"], c["M"], c["N"], c["K"]).split()[0].split("=")[1],
-             ms_per_step=wall_ms, kernel_ms=kern_ms,
+    r = dict(config=name, desc=c["desc"], dtype=c["dtype"], kernel=plan.split()[0].split("=")[1], plan=plan,
+             power=pwr, ms_per_step=wall_ms, kernel_ms=kern_ms,
              tflops=flops / (wall_ms * 1e-3) / 1e12, kernel_tflops=flops / (kern_ms * 1e-3) / 1e12,
              gbs=nbytes / (wall_ms * 1e-3) / 1e9, kernel_gbs=nbytes / (kern_ms * 1e-3) / 1e9)
+    if with_torch:
+        t = torch_same_device(torch.matmul, lambda i: (a, bs[i % nb]), steps, warmup, flops, nbytes, c.get("hbm"))
+        t["speedup"] = round(t["kernel_ms"] / kern_ms, 3)
+        r["torch_same_device"] = t
     del a, bs
     torch.cuda.empty_cache()
     return r
@@ -166,31 +331,24 @@ def caller_fn(c, cm):
     return lambda x, w, b: cm.conv2d(x, w, b)
 
 
-def time_caller(name: str, steps: int, warmup: int) -> dict:
+def time_caller(name: str, steps: int, warmup: int, with_torch: bool = True) -> dict:
     import torch
+    import torch.nn.functional as F
 
     import cmpext3
 
     c = CALLERS[name]
     args = caller_inputs(c, "cuda")
     fn = caller_fn(c, cmpext3)
-    for _ in range(warmup):
-        fn(*args)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(steps):
-        fn(*args)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    kern_ms = e0.elapsed_time(e1) / steps
+    wall_ms, kern_ms, pwr = timed_region(lambda i: fn(*args), steps, warmup)
     flops, nbytes = caller_algorithmic(c)
-    layout = "NK" if c["op"] == "linear" else "KN"
-    kernel = cmpext3.plan(c["dtype"], c["M"], c["N"], c["K"], layout=layout, batch=c["batch"],
-                          has_bias=c["op"] != "bmm").split()[0].split("=")[1]
+    plan = cmpext3.last_plan()
+    kernel = plan.split()[0].split("=")[1]
+    ref = None
+    if with_torch:
+        tfn = {"linear": F.linear, "bmm": torch.bmm, "conv": F.conv2d}[c["op"]]
+        ref = torch_same_device(tfn, lambda i: args, steps, warmup, flops, nbytes, c.get("hbm"))
+        ref["speedup"] = round(ref["kernel_ms"] / kern_ms, 3)
     del args
     torch.cuda.empty_cache()
     if c.get("hbm"):
@@ -198,116 +356,164 @@ def time_caller(name: str, steps: int, warmup: int) -> dict:
     else:
         ach, peak, unit, bound = flops / (kern_ms * 1e-3) / 1e12, PEAK[c["dtype"]], "TFLOP/s", "mfma"
     val = nbytes / (wall_ms * 1e-3) / 1e9 if c.get("hbm") else flops / (wall_ms * 1e-3) / 1e12
-    return {"desc": c["desc"], "kernel": kernel, "ms_per_step": round(wall_ms, 5), unit: round(val, 2),
+    return {"desc": c["desc"], "kernel": kernel, "plan": plan, "ms_per_step": round(wall_ms, 5),
+            unit: round(val, 2),
             "roofline": {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
                          "frac": round(ach / peak, 4), "traffic": load_traffic(name), "kernel": kernel,
-                         "kernel_ms": round(kern_ms, 5)}}
+                         "kernel_ms": round(kern_ms, 5), **clock_normalised(ach, peak, bound, pwr)},
+            "power": pwr, **({"torch_same_device": ref} if ref else {})}
+
+
+def cpu_description() -> str:
+    """CPU model, thread count and the ISA extensions that decide which torch CPU
+    kernels 16-bit products can use (oneDNN's fp16/bf16 paths)."""
+    import platform
+
+    import torch
+
+    model, flags = "", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and not model:
+                    model = line.split(":", 1)[1].strip()
+                if line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        model = platform.processor()
+    isa = [x for x in ("avx512f", "avx512_bf16", "avx512_fp16", "amx_bf16", "amx_fp16") if x in flags]
+    return (f"{model}; os.cpu_count()={os.cpu_count()}, torch threads={torch.get_num_threads()}; "
+            f"torch {torch.__version__}, oneDNN available={torch.backends.mkldnn.is_available()}; "
+            f"ISA: {' '.join(isa) or 'none of avx512f/avx512_bf16/avx512_fp16/amx'}")
+
+
+def sample_rate(run, limit: int, budget_s: float, start: int = 8, probe_s: float = 0.2,
+                sizes: tuple[int, int] | None = None, min_calls: int = 2) -> dict:
+    """Times `run(n)` (work on the first n rows of a workload; returns its work in the
+    metric's unit) on two sample sizes: n grows by 4x from `start` until a call takes
+    `probe_s` or n reaches `limit`, then the last two sizes (or n/2 and n) are each
+    repeated for about budget_s / 2 (at least twice, counting the probe).  Returns the
+    median rate of each size, so that the assumption that the rate per row does not
+    depend on the sample size can be checked.  `sizes` fixes the two sizes instead
+    (no probing), each timed at least `min_calls` times."""
+    timing = {}
+
+    def once(n):
+        t0 = time.perf_counter()
+        work = run(n)
+        dt = time.perf_counter() - t0
+        timing.setdefault(n, [work, []])[1].append(dt)
+        return dt
+
+    run(1)  # warm-up (first-call overheads)
+    if sizes is None:
+        n = min(start, limit)
+        probed = []
+        while True:
+            dt = once(n)
+            probed.append(n)
+            if dt >= probe_s or n >= limit:
+                break
+            n = min(limit, 4 * n)
+        if len(probed) == 1 and n > 1:
+            probed = [max(1, n // 2), n]
+        pair = probed[-2:]
+    else:
+        pair = list(sizes)
+    for m in pair:
+        t_start = time.perf_counter()
+        while len(timing.get(m, [0, []])[1]) < min_calls or (time.perf_counter() - t_start < budget_s / 2
+                                                            and len(timing[m][1]) < 20):
+            once(m)
+    return {m: (timing[m][0], statistics.median(timing[m][1]), len(timing[m][1])) for m in pair}
+
+
+def rate_summary(rates: dict, unit: str, what: str) -> dict:
+    """cpu_baseline object from sample_rate's two sizes: the value of the larger sample,
+    both samples listed, and the ratio of their rates (1.0 = proportional)."""
+    (n1, (w1, t1, c1)), (n2, (w2, t2, c2)) = sorted(rates.items())[0], sorted(rates.items())[-1]
+    r1, r2 = w1 / t1, w2 / t2
+    import torch
+
+    return {"value": round(r2, 6), "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{what}, rows 0..{n2 - 1}; median of {c2} calls ({t2 * 1e3:.1f} ms/call)",
+            "samples": [{"rows": n1, "ms_per_call": round(t1 * 1e3, 2), "value": round(r1, 6), "calls": c1},
+                        {"rows": n2, "ms_per_call": round(t2 * 1e3, 2), "value": round(r2, 6), "calls": c2}],
+            "rate_ratio_large_over_small": round(r2 / r1, 3) if r1 > 0 else None,
+            "host": cpu_description()}
 
 
 def cpu_caller(name: str, budget_s: float = 3.0) -> dict:
     """The same caller on CPU tensors (torch.nn.functional.linear, torch.bmm,
-    torch.nn.functional.conv2d), on a bounded sample: the first `n` rows of x
-    (linear), of batch entry 0's A (bmm) or of image 0 (conv), with `n` grown
-    until one call takes about half a second, then repeated for about
-    `budget_s` seconds.  Throughput per row equals that of the full problem."""
+    torch.nn.functional.conv2d) on two bounded samples: the first n rows of x
+    (linear), of batch entry 0's A (bmm) or of image 0 (conv)."""
     import torch
     import torch.nn.functional as F
 
     c = CALLERS[name]
     args = caller_inputs(c, "cpu")
-    Bn, M, N, K = c["batch"], c["M"], c["N"], c["K"]
+    M, N, K = c["M"], c["N"], c["K"]
     hw = int(round(N ** 0.5))
     limit = {"linear": M, "bmm": M, "conv": hw}[c["op"]]
+    hbm = c.get("hbm")
 
     def run(n):
         if c["op"] == "linear":
             F.linear(args[0][:n], args[1], args[2])
-            return 2.0 * n * N * K, "F.linear on CPU of rows 0..{} of x @ the full W^T + b"
+            return 2.0 * n * N * K / 1e12
         if c["op"] == "bmm":
             torch.bmm(args[0][:1, :n], args[1][:1])
-            return 2.0 * n * N * K, "torch.bmm on CPU of rows 0..{} of batch entry 0 @ its full B"
+            return 2.0 * n * N * K / 1e12
         F.conv2d(args[0][:1, :, :n], args[1], args[2])
-        return 2.0 * n * hw * M * K, "F.conv2d (1x1) on CPU of image rows 0..{} of image 0"
+        # bytes of the sample: its input rows, output rows, weight and bias (GB)
+        return 2.0 * (n * hw * K + n * hw * M + M * K + M) / 1e9 if hbm else 2.0 * n * hw * M * K / 1e12
 
-    n = min(8, limit)
-    while True:
-        t0 = time.perf_counter()
-        run(n)
-        dt = time.perf_counter() - t0
-        if dt > 0.5 or n >= limit:
-            break
-        n = min(limit, n * 4)
-    times = []
-    t_start = time.perf_counter()
-    while (len(times) < 3 or time.perf_counter() - t_start < budget_s) and len(times) < 50:
-        t0 = time.perf_counter()
-        flops, what = run(n)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    if c.get("hbm"):
-        # bytes of the sample: its input rows, output rows, weight and bias
-        nbytes = 2.0 * (n * hw * K + n * hw * M + M * K + M)
-        value, unit = nbytes / med / 1e9, "GB/s"
-    else:
-        value, unit = flops / med / 1e12, "TFLOP/s"
-    return {"value": round(value, 4), "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
-            "sample": what.format(n - 1) + f" ({c['dtype']}); median of {len(times)} calls "
-                      f"({med * 1e3:.1f} ms/call); os.cpu_count()={os.cpu_count()}"}
+    what = {"linear": f"F.linear on CPU ({c['dtype']}): x rows @ the full W^T + b",
+            "bmm": f"torch.bmm on CPU ({c['dtype']}): rows of batch entry 0 @ its full B",
+            "conv": f"F.conv2d 1x1 on CPU ({c['dtype']}): image rows of image 0"}[c["op"]]
+    return rate_summary(sample_rate(run, limit, budget_s), "GB/s" if hbm else "TFLOP/s", what)
 
 
-def log(msg: str) -> None:
-    print(f"bench: {msg}", file=sys.stderr, flush=True)
-
-
-def cpu_baseline(name: str, budget_s: float = 10.0) -> dict:
-    """The reference CPU path (torch.matmul on CPU) on a bounded sample of
-    the same workload: the first `rows` rows of A times all of B, with `rows`
-    grown from 8 until one call takes about a second (or A is exhausted), then
-    repeated for about `budget_s` seconds.  Throughput per row is the same as
-    for the full problem (every row of C costs 2*N*K flop and the same B)."""
-    import platform
-
-    import torch
+def cpu_baseline(name: str, budget_s: float = 8.0) -> dict:
+    """The reference CPU path that BASELINE.json names -- torch.matmul on CPU tensors in
+    the config's dtype (oracle.gemm_oracle.cpu_matmul) -- on two row samples of the
+    same workload (the first n rows of A times all of B).  For the HBM-bound config
+    the value is GB/s of the sample's own bytes (its rows of A and C, all of B)."""
+    import torch  # noqa: F401
 
     from oracle.gemm_oracle import cpu_matmul, make_inputs
 
     c = CONFIGS[name]
     a, b = make_inputs(c["dtype"], c["M"], c["N"], c["K"], c["dist"], c.get("scale", 1.0), 0)
-    rows = min(8, c["M"])
-    while True:
-        t0 = time.perf_counter()
-        cpu_matmul(a[:rows], b)
-        dt = time.perf_counter() - t0
-        log(f"cpu baseline probe: {rows} rows in {dt:.3f} s")
-        if dt > 1.0 or rows >= c["M"]:
-            break
-        rows = min(c["M"], rows * 4)
-    times = []
-    t_start = time.perf_counter()
-    while (len(times) < 3 or time.perf_counter() - t_start < budget_s) and len(times) < 50:
-        t0 = time.perf_counter()
-        cpu_matmul(a[:rows], b)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
     esz = 4 if c["dtype"] == "fp32" else 2
-    flops = 2.0 * rows * c["N"] * c["K"]
-    nbytes = float(esz * (rows * c["K"] + c["K"] * c["N"] + rows * c["N"]))
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        model = platform.processor()
     hbm = c.get("hbm")
-    return {"value": round((nbytes / med / 1e9) if hbm else (flops / med / 1e12), 4),
-            "unit": "GB/s" if hbm else "TFLOP/s",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"torch.matmul on CPU ({c['dtype']}) of rows 0..{rows - 1} of A ({rows}x{c['K']}) "
-                      f"@ the full B ({c['K']}x{c['N']}) of {name}; median of {len(times)} calls "
-                      f"({med * 1e3:.1f} ms/call) after a warm-up; os.cpu_count()={os.cpu_count()}; {model}"}
+
+    def run(n):
+        cpu_matmul(a[:n], b)
+        if hbm:
+            return esz * (n * c["K"] + c["K"] * c["N"] + n * c["N"]) / 1e9
+        return 2.0 * n * c["N"] * c["K"] / 1e12
+
+    log(f"cpu baseline {name}")
+    # GB/s of a row sample is not that of the whole (all of B is read for any rows): the
+    # HBM-bound config (M = 16) is timed whole, beside its first half
+    rates = sample_rate(run, c["M"], budget_s, sizes=(c["M"] // 2, c["M"]) if hbm else None,
+                        min_calls=1 if hbm else 2)
+    return rate_summary(rates, "GB/s" if hbm else "TFLOP/s",
+                        f"torch.matmul on CPU ({c['dtype']}) of A rows @ the full B ({c['K']}x{c['N']}) of {name}")
+
+
+def torch_same_device(fn, args_fn, steps: int, warmup: int, flops: float, nbytes: float, hbm: bool) -> dict:
+    """The same op through torch on the same GPU (hipBLASLt / MIOpen), timed like ours
+    -- the reference harness's comparison (tools/bench.py:67-104, speedup at :172).
+    Context only: never part of the measured path."""
+    wall_ms, kern_ms, _ = timed_region(lambda i: fn(*args_fn(i)), steps, warmup, power_window_s=0.0)
+    out = {"ms_per_step": round(wall_ms, 5), "kernel_ms": round(kern_ms, 5)}
+    if hbm:
+        out["GB/s"] = round(nbytes / (kern_ms * 1e-3) / 1e9, 1)
+    else:
+        out["TFLOP/s"] = round(flops / (kern_ms * 1e-3) / 1e12, 2)
+    return out
 
 
 def load_traffic(name: str):
@@ -321,6 +527,16 @@ def load_traffic(name: str):
         return None
 
 
+def clock_normalised(ach: float, peak: float, bound: str, pwr: dict) -> dict:
+    """For MFMA-bound work: the fraction of the matrix peak at the shader clock
+    measured during the timed steps (peak x sclk / 2400 MHz); the nominal `frac`
+    stays the record."""
+    sclk = pwr.get("avg_sclk_mhz") if pwr else None
+    if bound != "mfma" or not sclk:
+        return {}
+    return {"frac_at_sustained_sclk": round(ach / (peak * sclk / 2400.0), 4), "sustained_sclk_mhz": sclk}
+
+
 def roofline(r: dict, name: str) -> dict:
     c = CONFIGS[name]
     if c.get("hbm"):
@@ -329,7 +545,7 @@ def roofline(r: dict, name: str) -> dict:
         ach, peak, unit, bound = r["kernel_tflops"], PEAK[c["dtype"]], "TFLOP/s", "mfma"
     return {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
             "frac": round(ach / peak, 4), "traffic": load_traffic(name), "kernel": r["kernel"],
-            "kernel_ms": round(r["kernel_ms"], 5)}
+            "kernel_ms": round(r["kernel_ms"], 5), **clock_normalised(ach, peak, bound, r["power"])}
 
 
 def main() -> int:
@@ -343,6 +559,13 @@ def main() -> int:
     ap.add_argument("--no-others", action="store_true", help="time only the headline workload (no other "
                     "configs, no callers)")
     ap.add_argument("--no-callers", action="store_true", help="skip the linear / bmm / conv2d callers")
+    ap.add_argument("--no-torch", action="store_true", help="skip timing the same ops through torch on the GPU")
+    ap.add_argument("--headline-first", action="store_true",
+                    help="time the headline workload before the other configs and callers (by default it is "
+                         "timed last, once the GPU's clocks have left their idle state)")
+    ap.add_argument("--power-window", type=float, default=POWER_WINDOW_S, metavar="S",
+                    help="after each workload's timed steps, run it back to back for S seconds while reading "
+                         "board power and shader clock (0: skip)")
     ap.add_argument("--caller", default=None, choices=sorted(CALLERS),
                     help="time only this caller and print its JSON object (for profiling)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -373,27 +596,39 @@ def main() -> int:
         log(f"timing {args.caller} ({args.warmup} warm-up + {args.steps} steps)")
         print(json.dumps({args.caller: time_caller(args.caller, args.steps, args.warmup)}), flush=True)
         return 0
-    log(f"timing {args.config} ({args.warmup} warm-up + {args.steps} steps)")
-    head = time_gpu(args.config, args.steps, args.warmup)
-    log(f"{args.config}: {head['ms_per_step']:.4f} ms/step, {head['tflops']:.1f} TFLOP/s, {head['gbs']:.0f} GB/s")
+    with_torch = not args.no_torch
+    set_power_window(args.power_window)
+
+    def headline():
+        log(f"timing {args.config} ({args.warmup} warm-up + {args.steps} steps)")
+        r = time_gpu(args.config, args.steps, args.warmup, with_torch)
+        log(f"{args.config}: {r['ms_per_step']:.4f} ms/step, {r['tflops']:.1f} TFLOP/s, {r['gbs']:.0f} GB/s, "
+            f"power {r['power']}")
+        return r
+
+    head = headline() if args.headline_first or args.no_others else None
     others = {}
     if not args.no_others:
         for name in CONFIGS:
             if name != args.config:
                 log(f"timing {name}")
-                r = time_gpu(name, args.steps, args.warmup)
+                r = time_gpu(name, args.steps, args.warmup, with_torch)
                 log(f"{name}: {r['ms_per_step']:.4f} ms/step, {r['tflops']:.1f} TFLOP/s, {r['gbs']:.0f} GB/s")
                 c = CONFIGS[name]
-                others[name] = {"desc": r["desc"], "kernel": r["kernel"], "ms_per_step": round(r["ms_per_step"], 5),
+                others[name] = {"desc": r["desc"], "kernel": r["kernel"], "plan": r["plan"],
+                                "ms_per_step": round(r["ms_per_step"], 5),
                                 **({"GB/s": round(r["gbs"], 1)} if c.get("hbm") else
                                    {"TFLOP/s": round(r["tflops"], 2)}),
-                                "roofline": roofline(r, name)}
+                                "roofline": roofline(r, name), "power": r["power"],
+                                **({"torch_same_device": r["torch_same_device"]} if with_torch else {})}
     callers = {}
     if not args.no_others and not args.no_callers:
         for name in CALLERS:
             log(f"timing {name}")
-            callers[name] = time_caller(name, args.steps, args.warmup)
+            callers[name] = time_caller(name, args.steps, args.warmup, with_torch)
             log(f"{name}: {callers[name]['ms_per_step']:.4f} ms/step")
+    if head is None:
+        head = headline()
     c = CONFIGS[args.config]
     hbm = c.get("hbm")
     line = {
@@ -410,13 +645,18 @@ def main() -> int:
         "dtype": {"fp16": "f16", "bf16": "bf16", "fp32": "f32"}[c["dtype"]],
         "data": "synthetic (seeded torch.randn / torch.rand on the GPU, BASELINE.json distributions)",
         "config": {"workload": f"{args.config}: {c['desc']}", "M": c["M"], "N": c["N"], "K": c["K"],
-                   "accumulate": "fp32", "kernel": head["kernel"]},
+                   "accumulate": "fp32", "kernel": head["kernel"], "plan": head["plan"]},
         "roofline": roofline(head, args.config),
+        "power": head["power"],
     }
+    if with_torch:
+        line["torch_same_device"] = head["torch_same_device"]
     if not args.no_cpu:
-        log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(args.config)
     if others:
+        if not args.no_cpu:
+            for name in others:
+                others[name]["cpu_baseline"] = cpu_baseline(name)
         line["other_configs"] = others
     if callers:
         if not args.no_cpu:

@@ -9,6 +9,7 @@ GEMM entry points, src/main.cpp:1594-1602, plus the dtype-specific matmuls):
     conv2d(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1)
                                                                1x1 NCHW convolution as a GEMM
     plan(dtype, M, N, K, layout="KN", batch=1, has_bias=False) kernel the selector picks
+    last_plan()                                                kernel(s) this thread's last call ran
 
 Every call runs the hand-written gfx950 kernels of lib/libcmpext3_gemm.so on
 PyTorch's current stream.  There is no fallback: if the compiled extension is
@@ -17,7 +18,8 @@ the `build` submodule stays usable.
 """
 import torch  # noqa: F401  (loads PyTorch's HIP runtime before the extension binds to it)
 
-__all__ = ["fp16_matmul", "bf16_matmul", "fp32_matmul", "linear", "bmm", "conv2d", "plan", "version"]
+__all__ = ["fp16_matmul", "bf16_matmul", "fp32_matmul", "linear", "bmm", "conv2d", "plan", "last_plan",
+           "version"]
 
 try:
     from . import _cmpext3 as _ext
@@ -37,6 +39,7 @@ if _ext is not None:
     bmm = _ext.bmm
     conv2d = _ext.conv2d
     plan = _ext.plan
+    last_plan = _ext.last_plan
     version = _ext.version
     extension_path = _ext.__file__
 else:

@@ -16,7 +16,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libc
 
 F16, BF16, F32 = 0, 1, 2
 B_KN, B_NK = 0, 1
-OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_TOO_LARGE = 0, -1, -2, -3
+OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_TOO_LARGE, ERR_WORKSPACE = 0, -1, -2, -3, -4
+BIAS_PER_ROW = 1
 
 # Exported symbols and their C signatures, as declared in include/cmpext3_gemm.h.
 _i, _i64, _p, _cp = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_char_p
@@ -32,6 +33,11 @@ SIGNATURES = {
     "cmpext3_conv2d_1x1": (_i, [_i, _p, _p, _p, _p, _i, _i, _i, _i, _p, _i64, _p]),
     "cmpext3_gemm_workspace_size": (_i64, [_i, _i, _i, _i, _i, _i]),
     "cmpext3_gemm_plan": (_i, [_i, _i, _i, _i, _i, _i64, _i64, _i64, _i, _i, _i, _i64, _cp, _i]),
+    "cmpext3_gemm_prepare": (_i, [_p, _i, _i, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i,
+                                  _i, _i, _i, _i, _i64]),
+    "cmpext3_gemm_call_workspace_size": (_i64, [_p]),
+    "cmpext3_gemm_call_describe": (_i, [_p, _cp, _i]),
+    "cmpext3_gemm_run": (_i, [_p, _p, _i64, _p]),
     "cmpext3_status_string": (_cp, [_i]),
     "cmpext3_version": (_cp, []),
 }
@@ -73,8 +79,10 @@ def workspace_size(dtype: int, layout: int, M: int, N: int, K: int, batch: int =
     return lib().cmpext3_gemm_workspace_size(dtype, layout, M, N, K, batch)
 
 
-def _stream_handle(stream) -> int:
+def _stream_handle(stream) -> int | None:
     if stream is None:
+        if not torch.cuda.is_available():  # argument checks on a machine without a GPU
+            return None
         stream = torch.cuda.current_stream()
     return stream.cuda_stream
 
@@ -92,6 +100,46 @@ def gemm_ex(dtype: int, layout: int, A, lda: int, stride_a: int, B, ldb: int, st
     return lib().cmpext3_gemm_ex(dtype, layout, ptr(A), lda, stride_a, ptr(B), ldb, stride_b, ptr(C),
                                  ldc, stride_c, ptr(bias), M, N, K, batch, ptr(workspace), ws_bytes,
                                  _stream_handle(stream))
+
+
+class Call(ctypes.Structure):
+    """cmpext3_gemm_call: one prepared GEMM (opaque, 512 bytes)."""
+    _fields_ = [("opaque", ctypes.c_int64 * 64)]
+
+
+def _ptr(x):
+    if x is None:
+        return None
+    return x.data_ptr() if hasattr(x, "data_ptr") else int(x)
+
+
+def prepare(dtype: int, layout: int, A, lda: int, stride_a: int, B, ldb: int, stride_b: int, C,
+            ldc: int, stride_c: int, bias, M: int, N: int, K: int, batch: int = 1, flags: int = 0,
+            workspace_limit: int = (1 << 63) - 1) -> tuple[int, Call]:
+    """cmpext3_gemm_prepare: returns (status, call)."""
+    call = Call()
+    st = lib().cmpext3_gemm_prepare(ctypes.byref(call), dtype, layout, _ptr(A), lda, stride_a, _ptr(B), ldb,
+                                    stride_b, _ptr(C), ldc, stride_c, _ptr(bias), flags, M, N, K, batch,
+                                    workspace_limit)
+    return st, call
+
+
+def call_workspace_size(call: Call) -> int:
+    return lib().cmpext3_gemm_call_workspace_size(ctypes.byref(call))
+
+
+def describe(call: Call) -> tuple[int, str]:
+    buf = ctypes.create_string_buffer(256)
+    kid = lib().cmpext3_gemm_call_describe(ctypes.byref(call), buf, 256)
+    return kid, buf.value.decode()
+
+
+def run(call: Call, workspace=None, workspace_bytes: int | None = None, stream=None) -> int:
+    """cmpext3_gemm_run; `workspace` is None or a device tensor (its byte size is passed
+    unless `workspace_bytes` says otherwise)."""
+    if workspace_bytes is None:
+        workspace_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    return lib().cmpext3_gemm_run(ctypes.byref(call), _ptr(workspace), workspace_bytes, _stream_handle(stream))
 
 
 def conv2d_1x1(dtype: int, inp, weight, bias, out, batch: int, c_in: int, c_out: int, hw: int,

@@ -7,6 +7,8 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <string>
+#include <type_traits>
 
 #include "../../include/cmpext3_gemm.h"
 #include "kernels.h"
@@ -78,12 +80,26 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
 }
 
 constexpr int64_t kMaxGridZ = 65535;
+constexpr uint64_t kCallMagic = 0x636d7065787433ull;  // "cmpext3"
 
-// Shared body of cmpext3_gemm_ex (bias per column) and cmpext3_conv2d_1x1
-// (bias per row).
-int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb,
-             int64_t stride_b, void* C, int64_t ldc, int64_t stride_c, const void* bias, int bias_row, int M, int N,
-             int K, int batch, void* workspace, int64_t workspace_bytes, void* stream) {
+// The contents of a cmpext3_gemm_call: one validated, planned GEMM.
+struct Prepared {
+  uint64_t magic;
+  Request r;
+  Plan plan;
+  const void* A;
+  const void* B;
+  void* C;
+  const void* bias;
+  int bias_row;
+  bool empty;  // M, N or batch is 0: nothing to launch
+};
+static_assert(sizeof(Prepared) <= sizeof(cmpext3_gemm_call), "cmpext3_gemm_call too small");
+static_assert(std::is_trivially_copyable<Prepared>::value, "cmpext3_gemm_call is copied bytewise");
+
+int prepare(Prepared* pc, int dtype, int b_layout, const void* A, int64_t lda, int64_t stride_a, const void* B,
+            int64_t ldb, int64_t stride_b, void* C, int64_t ldc, int64_t stride_c, const void* bias, int bias_row,
+            int M, int N, int K, int batch, int64_t workspace_limit) {
   Request r{};
   r.dtype = dtype;
   r.layout = b_layout;
@@ -96,22 +112,55 @@ int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride
   r.stride_a = stride_a;
   r.stride_b = stride_b;
   r.stride_c = stride_c;
-  r.align = std::min(std::min(align_of(A), align_of(B)), std::min(align_of(C), align_of(bias)));
+  // the bias is read element by element where its address needs it (tile kernels:
+  // GemmParams::bias_vec), so only A, B and C steer the kernel choice
   r.align_a = align_of(A);
   r.align_b = align_of(B);
-  r.align_c = std::min(align_of(C), align_of(bias));
+  r.align_c = align_of(C);
+  r.align = std::min(std::min(r.align_a, r.align_b), r.align_c);
   r.has_bias = bias != nullptr;
   r.batch = batch;
-  r.ws_bytes = (workspace != nullptr && align_of(workspace) >= 16) ? workspace_bytes : 0;
+  r.ws_bytes = std::max<int64_t>(0, workspace_limit);
   Plan plan;
   const int st = make_plan(r, &plan);
   if (st != CMPEXT3_OK) return st;
-  if (M == 0 || N == 0 || batch == 0) return CMPEXT3_OK;
-  if (C == nullptr || (K > 0 && (A == nullptr || B == nullptr))) return CMPEXT3_ERR_INVALID_ARG;
+  const bool empty = M == 0 || N == 0 || batch == 0;
+  if (!empty && (C == nullptr || (K > 0 && (A == nullptr || B == nullptr)))) return CMPEXT3_ERR_INVALID_ARG;
+  if (empty) plan.ws_bytes = 0;
+  Prepared p{};
+  p.magic = kCallMagic;
+  p.r = r;
+  p.plan = plan;
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  p.bias = bias;
+  p.bias_row = bias_row;
+  p.empty = empty;
+  *pc = p;
+  return CMPEXT3_OK;
+}
 
+const Prepared* as_prepared(const cmpext3_gemm_call* call) {
+  if (call == nullptr) return nullptr;
+  const Prepared* pc = reinterpret_cast<const Prepared*>(call);
+  return pc->magic == kCallMagic ? pc : nullptr;
+}
+
+// Enqueues a prepared call: the zero-padded operand copies it planned, then its
+// kernel(s), batch entries in chunks of at most 65535 grid rows.
+int run(const Prepared& pc, void* workspace, int64_t workspace_bytes, hipStream_t s) {
+  const Plan& plan = pc.plan;
+  if (pc.empty) return CMPEXT3_OK;
+  if (plan.ws_bytes > 0 && (workspace == nullptr || align_of(workspace) < 16 || workspace_bytes < plan.ws_bytes))
+    return CMPEXT3_ERR_WORKSPACE;
+  const int dtype = pc.r.dtype, b_layout = pc.r.layout;
+  const int M = (int)pc.r.M, N = (int)pc.r.N, batch = (int)pc.r.batch;
+  int K = (int)pc.r.K;
+  const void* A = pc.A;
+  const void* B = pc.B;
+  int64_t lda = pc.r.lda, ldb = pc.r.ldb, stride_a = pc.r.stride_a, stride_b = pc.r.stride_b;
   const int64_t esz = dtype == kF32 ? 4 : 2;
-  hipStream_t s = (hipStream_t)stream;
-  // zero-padded aligned copies of unaligned operands (planned by make_plan)
   char* ws = (char*)workspace;
   const bool kn = b_layout == CMPEXT3_B_KN;
   if (plan.pad_a) {
@@ -137,16 +186,16 @@ int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride
     ws += plan.pad_b_bytes;
   }
   if (plan.pad_a || plan.pad_b) K = (int)plan.kp;
-  workspace = ws;
   GemmParams p{};
-  p.bias = bias;
-  p.bias_row = bias_row;
+  p.bias = pc.bias;
+  p.bias_row = pc.bias_row;
+  p.bias_vec = pc.bias != nullptr && align_of(pc.bias) >= 8;
   p.lda = lda;
   p.ldb = ldb;
-  p.ldc = ldc;
+  p.ldc = pc.r.ldc;
   p.stride_a = stride_a;
   p.stride_b = stride_b;
-  p.stride_c = stride_c;
+  p.stride_c = pc.r.stride_c;
   p.M = M;
   p.N = N;
   p.K = K;
@@ -161,12 +210,25 @@ int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride
     const int64_t nb = std::min<int64_t>(zmax, batch - b0);
     p.A = (const char*)A + b0 * stride_a * esz;
     p.B = (const char*)B + b0 * stride_b * esz;
-    p.C = (char*)C + b0 * stride_c * esz;
+    p.C = (char*)pc.C + b0 * pc.r.stride_c * esz;
     const dim3 grid((unsigned)(plan.tiles_m * plan.tiles_n), 1, (unsigned)nb);
-    const hipError_t e = dispatch(plan, dtype, b_layout, p, grid, workspace, s);
+    const hipError_t e = dispatch(plan, dtype, b_layout, p, grid, ws, s);
     if (e != hipSuccess) return (int)e;
   }
   return CMPEXT3_OK;
+}
+
+// Shared body of cmpext3_gemm_ex (bias per column) and cmpext3_conv2d_1x1
+// (bias per row): prepare with the workspace at hand, then run.
+int run_gemm(int dtype, int b_layout, const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb,
+             int64_t stride_b, void* C, int64_t ldc, int64_t stride_c, const void* bias, int bias_row, int M, int N,
+             int K, int batch, void* workspace, int64_t workspace_bytes, void* stream) {
+  Prepared pc;
+  const int64_t limit = (workspace != nullptr && align_of(workspace) >= 16) ? workspace_bytes : 0;
+  const int st = prepare(&pc, dtype, b_layout, A, lda, stride_a, B, ldb, stride_b, C, ldc, stride_c, bias, bias_row,
+                         M, N, K, batch, limit);
+  if (st != CMPEXT3_OK) return st;
+  return run(pc, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 }  // namespace
@@ -177,6 +239,43 @@ extern "C" int cmpext3_gemm_ex(int dtype, int b_layout, const void* A, int64_t l
                                void* workspace, int64_t workspace_bytes, void* stream) {
   return run_gemm(dtype, b_layout, A, lda, stride_a, B, ldb, stride_b, C, ldc, stride_c, bias, 0, M, N, K, batch,
                   workspace, workspace_bytes, stream);
+}
+
+extern "C" int cmpext3_gemm_prepare(cmpext3_gemm_call* call, int dtype, int b_layout, const void* A, int64_t lda,
+                                    int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b, void* C,
+                                    int64_t ldc, int64_t stride_c, const void* bias, int flags, int M, int N, int K,
+                                    int batch, int64_t workspace_limit) {
+  if (call == nullptr || (flags & ~CMPEXT3_BIAS_PER_ROW) != 0) return CMPEXT3_ERR_INVALID_ARG;
+  memset(call, 0, sizeof *call);
+  Prepared pc;
+  const int st = prepare(&pc, dtype, b_layout, A, lda, stride_a, B, ldb, stride_b, C, ldc, stride_c, bias,
+                         (flags & CMPEXT3_BIAS_PER_ROW) ? 1 : 0, M, N, K, batch, workspace_limit);
+  if (st != CMPEXT3_OK) return st;
+  memcpy(call, &pc, sizeof pc);
+  return CMPEXT3_OK;
+}
+
+extern "C" int64_t cmpext3_gemm_call_workspace_size(const cmpext3_gemm_call* call) {
+  const Prepared* pc = as_prepared(call);
+  return pc ? pc->plan.ws_bytes : (int64_t)CMPEXT3_ERR_INVALID_ARG;
+}
+
+extern "C" int cmpext3_gemm_call_describe(const cmpext3_gemm_call* call, char* buf, int buflen) {
+  const Prepared* pc = as_prepared(call);
+  if (pc == nullptr) return CMPEXT3_ERR_INVALID_ARG;
+  if (buf && buflen > 0) {
+    const std::string d = describe(pc->r, pc->plan);
+    strncpy(buf, d.c_str(), (size_t)buflen - 1);
+    buf[buflen - 1] = '\0';
+  }
+  return (int)pc->plan.kernel;
+}
+
+extern "C" int cmpext3_gemm_run(const cmpext3_gemm_call* call, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  const Prepared* pc = as_prepared(call);
+  if (pc == nullptr) return CMPEXT3_ERR_INVALID_ARG;
+  return run(*pc, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 // NCHW 1x1 convolution = `batch` GEMMs out_b[c_out, hw] = W[c_out, c_in] * in_b[c_in, hw]
@@ -276,6 +375,9 @@ extern "C" const char* cmpext3_status_string(int status) {
     case CMPEXT3_ERR_INVALID_ARG: return "invalid argument (null pointer, negative size or leading dimension too small)";
     case CMPEXT3_ERR_UNSUPPORTED: return "unsupported dtype or B layout";
     case CMPEXT3_ERR_TOO_LARGE: return "size or leading dimension exceeds the kernels' 32-bit offset range";
+    case CMPEXT3_ERR_WORKSPACE:
+      return "workspace missing, not 16-byte aligned or smaller than the prepared call needs "
+             "(cmpext3_gemm_call_workspace_size)";
     default:
       if (status > 0) return hipGetErrorString((hipError_t)status);
       return "unknown status";

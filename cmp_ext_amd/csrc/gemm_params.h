@@ -17,6 +17,7 @@ struct GemmParams {
   void* C;
   const void* bias;  // nullptr, or a vector of the input dtype added before rounding:
   int bias_row;      //   0: N elements, one per column of C (Linear); 1: M elements, one per row (conv 1x1)
+  int bias_vec;      // the bias address is 8-byte aligned (per-column bias read four elements at a time)
   int64_t lda, ldb, ldc;
   int64_t stride_a, stride_b, stride_c;  // batch strides (grid.z)
   int M, N, K;

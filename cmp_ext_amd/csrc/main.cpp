@@ -2,8 +2,9 @@
 // surface of the MI355X GEMM library.  It mirrors the GEMM part of the
 // reference bindings (src/main.cpp:155-357, :1594-1602) and adds the three
 // dtype-specific matmul entry points.  Tensor checks and output allocation
-// happen here; every product goes through the C ABI (cmpext3_gemm_ex), which
-// launches the hand-written gfx950 kernels on PyTorch's current stream.
+// happen here; every product goes through the C ABI (cmpext3_gemm_prepare, then
+// cmpext3_gemm_run with the workspace the plan asks for), which launches the
+// hand-written gfx950 kernels on PyTorch's current stream.
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
@@ -38,13 +39,34 @@ int64_t checked_int(int64_t v, const char* what) {
   return v;
 }
 
-// Workspace for cmpext3_gemm_ex (the skinny-M path splits K into fp32
-// partials), from PyTorch's caching allocator on the operands' device.
-torch::Tensor workspace_for(int code, int layout, int64_t M, int64_t N, int64_t K, int64_t batch,
-                            const torch::Tensor& like) {
-  const int64_t bytes = cmpext3_gemm_workspace_size(code, layout, (int)M, (int)N, (int)K, (int)batch);
-  if (bytes <= 0) return torch::Tensor();
-  return torch::empty({bytes}, like.options().dtype(torch::kUInt8));
+// The prepared call each operator ran last on this thread (cmpext3.last_plan()).
+thread_local cmpext3_gemm_call g_last_call;
+thread_local bool g_has_last_call = false;
+
+// Runs a prepared call on PyTorch's current stream of `like`'s device with the
+// workspace its plan asks for (from PyTorch's caching allocator), so the
+// kernel is chosen once per operator call.
+void run_prepared(const cmpext3_gemm_call& call, const torch::Tensor& like, const char* op) {
+  const int64_t need = cmpext3_gemm_call_workspace_size(&call);
+  check_status(need < 0 ? (int)need : CMPEXT3_OK, op);
+  torch::Tensor ws;
+  if (need > 0) ws = torch::empty({need}, like.options().dtype(torch::kUInt8));
+  check_status(cmpext3_gemm_run(&call, ws.defined() ? ws.data_ptr() : nullptr, need, current_stream(like)), op);
+  g_last_call = call;
+  g_has_last_call = true;
+}
+
+// Prepares C = A * op(B) (+ bias) for this call's exact pointers, pitches and
+// strides (the bindings provide whatever workspace the plan wants) and runs it.
+void gemm(int code, int layout, const torch::Tensor& a, int64_t lda, int64_t stride_a, const torch::Tensor& b,
+          int64_t ldb, int64_t stride_b, torch::Tensor& c, int64_t ldc, int64_t stride_c, const void* bias,
+          int flags, int64_t M, int64_t N, int64_t K, int64_t batch, const char* op) {
+  cmpext3_gemm_call call;
+  check_status(cmpext3_gemm_prepare(&call, code, layout, a.data_ptr(), lda, stride_a, b.data_ptr(), ldb, stride_b,
+                                    c.data_ptr(), ldc, stride_c, bias, flags, (int)M, (int)N, (int)K, (int)batch,
+                                    INT64_MAX),
+               op);
+  run_prepared(call, a, op);
 }
 
 // A 2-D operand usable as row-major with unit inner stride: returns the row
@@ -93,12 +115,7 @@ torch::Tensor matmul_impl(const torch::Tensor& a_in, const torch::Tensor& b_in, 
     }
   }
   torch::Tensor c = torch::empty({M, N}, a.options());
-  const torch::Tensor ws = workspace_for(dtype_code(want), layout, M, N, K, 1, a);
-  const int st = cmpext3_gemm_ex(dtype_code(want), layout, a.data_ptr(), lda, 0, b.data_ptr(), ldb, 0,
-                                 c.data_ptr(), std::max<int64_t>(N, 1), 0, nullptr, (int)M, (int)N, (int)K,
-                                 1, ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws.numel() : 0,
-                                 current_stream(a));
-  check_status(st, op);
+  gemm(dtype_code(want), layout, a, lda, 0, b, ldb, 0, c, std::max<int64_t>(N, 1), 0, nullptr, 0, M, N, K, 1, op);
   return c;
 }
 
@@ -148,11 +165,8 @@ torch::Tensor linear(torch::Tensor input, const torch::Tensor& weight, c10::opti
   std::vector<int64_t> out_shape(input.sizes().begin(), input.sizes().end() - 1);
   out_shape.push_back(N);
   torch::Tensor out = torch::empty(out_shape, input.options());
-  const int st = cmpext3_gemm_ex(code, CMPEXT3_B_NK, input.data_ptr(), std::max<int64_t>(K, 1), 0,
-                                 w.data_ptr(), std::max<int64_t>(K, 1), 0, out.data_ptr(),
-                                 std::max<int64_t>(N, 1), 0, bias_ptr, (int)M, (int)N, (int)K, 1, nullptr, 0,
-                                 current_stream(input));
-  check_status(st, "linear");
+  gemm(code, CMPEXT3_B_NK, input, std::max<int64_t>(K, 1), 0, w, std::max<int64_t>(K, 1), 0, out,
+       std::max<int64_t>(N, 1), 0, bias_ptr, 0, M, N, K, 1, "linear");
   return out;
 }
 
@@ -179,13 +193,8 @@ torch::Tensor bmm(torch::Tensor input, torch::Tensor mat2) {
   input = input.contiguous();
   mat2 = mat2.contiguous();
   torch::Tensor out = torch::empty({Bn, M, N}, input.options());
-  const torch::Tensor ws = workspace_for(code, CMPEXT3_B_KN, M, N, K, Bn, input);
-  const int st = cmpext3_gemm_ex(code, CMPEXT3_B_KN, input.data_ptr(), std::max<int64_t>(K, 1), M * K,
-                                 mat2.data_ptr(), std::max<int64_t>(N, 1), K * N, out.data_ptr(),
-                                 std::max<int64_t>(N, 1), M * N, nullptr, (int)M, (int)N, (int)K, (int)Bn,
-                                 ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws.numel() : 0,
-                                 current_stream(input));
-  check_status(st, "bmm");
+  gemm(code, CMPEXT3_B_KN, input, std::max<int64_t>(K, 1), M * K, mat2, std::max<int64_t>(N, 1), K * N, out,
+       std::max<int64_t>(N, 1), M * N, nullptr, 0, M, N, K, Bn, "bmm");
   return out;
 }
 
@@ -252,11 +261,10 @@ torch::Tensor conv2d(torch::Tensor input, torch::Tensor weight, c10::optional<to
     bias_ptr = bias_c.data_ptr();
   }
   torch::Tensor out = torch::empty({Bn, Cout, H, W}, input.options());
-  const torch::Tensor ws = workspace_for(code, CMPEXT3_B_KN, Cout, hw, Cin, Bn, input);
-  const int st = cmpext3_conv2d_1x1(code, input.data_ptr(), weight.data_ptr(), bias_ptr, out.data_ptr(), (int)Bn,
-                                    (int)Cin, (int)Cout, (int)hw, ws.defined() ? ws.data_ptr() : nullptr,
-                                    ws.defined() ? ws.numel() : 0, current_stream(input));
-  check_status(st, "conv2d");
+  // the GEMMs of cmpext3_conv2d_1x1: out_b[C_out, HW] = W[C_out, C_in] * in_b[C_in, HW] for
+  // every image b, the weight shared (stride 0), the bias per output row
+  gemm(code, CMPEXT3_B_KN, weight, std::max<int64_t>(Cin, 1), 0, input, std::max<int64_t>(hw, 1), Cin * hw, out,
+       std::max<int64_t>(hw, 1), Cout * hw, bias_ptr, CMPEXT3_BIAS_PER_ROW, Cout, hw, Cin, Bn, "conv2d");
   return out;
 }
 
@@ -269,11 +277,20 @@ std::string plan(const std::string& dtype, int64_t M, int64_t N, int64_t K, cons
   const int lay = layout == "NK" ? CMPEXT3_B_NK : CMPEXT3_B_KN;
   const int64_t ldb = lay == CMPEXT3_B_KN ? N : K;
   char buf[256];
-  // the bindings always provide the workspace a plan asks for
+  // packed operands at 16-byte aligned addresses, and the workspace the plan asks for
+  // (what the bindings provide); cmpext3.last_plan() reports what a call actually ran
   const int st = cmpext3_gemm_plan(code, lay, (int)M, (int)N, (int)K, std::max<int64_t>(K, 1),
                                    std::max<int64_t>(ldb, 1), std::max<int64_t>(N, 1), 16, has_bias ? 1 : 0,
                                    (int)batch, INT64_MAX, buf, sizeof buf);
   TORCH_CHECK(st >= 0, "cmpext3.plan: ", cmpext3_status_string(st));
+  return std::string(buf);
+}
+
+std::string last_plan() {
+  TORCH_CHECK(g_has_last_call, "cmpext3.last_plan: no operator has run on this thread yet");
+  char buf[256];
+  const int st = cmpext3_gemm_call_describe(&g_last_call, buf, sizeof buf);
+  TORCH_CHECK(st >= 0, "cmpext3.last_plan: ", cmpext3_status_string(st));
   return std::string(buf);
 }
 
@@ -293,5 +310,8 @@ PYBIND11_MODULE(_cmpext3, m) {
   m.def("plan", &plan, "Describe the kernel chosen for a GEMM shape", py::arg("dtype"), py::arg("M"),
         py::arg("N"), py::arg("K"), py::arg("layout") = "KN", py::arg("batch") = 1,
         py::arg("has_bias") = false);
+  m.def("last_plan", &last_plan,
+        "Describe the kernel(s) the last operator call on this thread ran (its actual pointers, pitches and "
+        "workspace)");
   m.def("version", []() { return std::string(cmpext3_version()); });
 }

@@ -132,6 +132,8 @@ int make_plan_core(const Request& r, Plan* plan) {
   // Kernels address at most 256 rows of an operand from a per-tile base with
   // 32-bit byte offsets.
   if (256 * r.lda * esz > kIntMax || 256 * r.ldb * esz > kIntMax) return CMPEXT3_ERR_TOO_LARGE;
+  // The fp32 kernels store C the same way (the 16-bit ones through 64-bit pointers).
+  if (r.dtype == kF32 && 256 * r.ldc * esz > kIntMax) return CMPEXT3_ERR_TOO_LARGE;
   if (cdiv(r.M, 64) * cdiv(r.N, 64) > kIntMax) return CMPEXT3_ERR_TOO_LARGE;
 
   Plan p{};

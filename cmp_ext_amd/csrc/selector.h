@@ -35,8 +35,9 @@ struct Request {
   int64_t M, N, K;
   int64_t lda, ldb, ldc;
   int64_t stride_a, stride_b, stride_c;
-  int align;  // largest power of two (<= 16) dividing every operand address
-  int align_a, align_b, align_c;  // the same for A, B, and C with the bias (0: use `align`)
+  int align;  // largest power of two (<= 16) dividing the addresses of A, B and C
+  int align_a, align_b, align_c;  // the same for A, B and C alone (0: use `align`); the bias
+                                  // address never restricts the kernel choice
   bool b_cols_padded;             // B ([K, N]) has zero columns up to a multiple of 8 (planner use)
   bool has_bias;
   int64_t batch;

@@ -297,12 +297,13 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] += b;
     } else if constexpr (BIAS == 1) {
-      // four consecutive bias values: one 8-byte load when all four exist, else one
-      // 2-byte load each (a descriptor of 2N bytes returns zeros past N)
+      // four consecutive bias values: one 8-byte load when all four exist and the bias
+      // is 8-byte aligned, else one 2-byte load each (a descriptor of 2N bytes returns
+      // zeros past N)
       const int n = nw + 16 * j + 4 * G;
       const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(bias), 0, 2 * N, kBufWord3);
       u32x2 bb;
-      if (n + 4 <= N) {
+      if (n + 4 <= N && p.bias_vec) {
         bb = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(br, (uint32_t)(2 * n), 0, 0));
       } else {
         uint32_t h[4];

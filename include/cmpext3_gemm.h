@@ -32,6 +32,7 @@ extern "C" {
 #define CMPEXT3_ERR_INVALID_ARG (-1)  /* null pointer, negative size, bad stride */
 #define CMPEXT3_ERR_UNSUPPORTED (-2)  /* unknown dtype / layout */
 #define CMPEXT3_ERR_TOO_LARGE (-3)    /* a size or stride does not fit the kernels' 32-bit offsets */
+#define CMPEXT3_ERR_WORKSPACE (-4)    /* a prepared call got less (or less aligned) workspace than it needs */
 
 /* Element types. */
 #define CMPEXT3_F16 0
@@ -121,6 +122,43 @@ int cmpext3_gemm_ex(int dtype, int b_layout,
 int cmpext3_conv2d_1x1(int dtype, const void* input, const void* weight, const void* bias, void* output,
                        int batch, int c_in, int c_out, int hw,
                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Prepared calls: cmpext3_gemm_ex in two steps, so that a caller can size the
+ * workspace from the very plan that will run (the kernel is chosen once) and
+ * can see which kernel that is.
+ *
+ * cmpext3_gemm_prepare validates the arguments (those of cmpext3_gemm_ex, plus
+ * `flags`), picks the kernel and stores the whole call -- pointers, sizes and
+ * the plan -- in *call; nothing is launched and no GPU is touched.
+ * `workspace_limit` is the most workspace the caller is willing to provide
+ * (0: none; INT64_MAX: whatever helps).  CMPEXT3_BIAS_PER_ROW in `flags` adds
+ * the bias per row of C (M elements) instead of per column (N elements).
+ * cmpext3_gemm_call_workspace_size says how much workspace the chosen kernels
+ * need (<= workspace_limit), cmpext3_gemm_call_describe writes a one-line
+ * description of them and returns the kernel id, and cmpext3_gemm_run
+ * enqueues them on `stream` with a workspace of at least that many bytes
+ * (16-byte aligned; NULL when none is needed; CMPEXT3_ERR_WORKSPACE otherwise).
+ * A prepared call may be run more than once (e.g. while a graph is captured);
+ * the buffers it names must then still be valid.  cmpext3_gemm_ex(...) is
+ * cmpext3_gemm_prepare(..., workspace_bytes) followed by cmpext3_gemm_run.
+ * No counterpart in the reference, whose launchers take no workspace and
+ * choose nothing at run time (src/main.cpp:12-14, fp16_matmul.cu:12-22).
+ */
+#define CMPEXT3_BIAS_PER_ROW 1
+typedef struct cmpext3_gemm_call {
+  int64_t opaque[64];
+} cmpext3_gemm_call;
+
+int cmpext3_gemm_prepare(cmpext3_gemm_call* call, int dtype, int b_layout,
+                         const void* A, int64_t lda, int64_t stride_a,
+                         const void* B, int64_t ldb, int64_t stride_b,
+                         void* C, int64_t ldc, int64_t stride_c,
+                         const void* bias, int flags,
+                         int M, int N, int K, int batch, int64_t workspace_limit);
+int64_t cmpext3_gemm_call_workspace_size(const cmpext3_gemm_call* call);
+int cmpext3_gemm_call_describe(const cmpext3_gemm_call* call, char* buf, int buflen);
+int cmpext3_gemm_run(const cmpext3_gemm_call* call, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Bytes of workspace cmpext3_gemm_ex can use for these arguments (zero-padded

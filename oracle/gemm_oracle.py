@@ -30,7 +30,13 @@ rank-1 integer, K = 1, transpose and linearity identities).  conv2d_1x1_f64
 is checked against exactly rounded golden values, against
 torch.nn.functional.conv2d in float64 and against matmul_f64 per image.  The dtype
 rounding functions are checked against IEEE bit-level decoding in C and
-against exhaustive/boundary cases.
+against exhaustive/boundary cases.  make_inputs (the seeded benchmark inputs)
+is checked against the distributions BASELINE.json names -- Kolmogorov-Smirnov
+against scipy's uniform[-1, 1] and normal(0, scale) CDFs, range, mean and
+spread within a few standard errors -- and for the order of its draws (A
+first, then B from the same generator) and the independence of A and B;
+planted mistakes (rand for randn, a wrong scale, a [0, 1) range, B equal to A)
+each fail those checks.
 """
 from __future__ import annotations
 
@@ -65,13 +71,6 @@ def round_bf16(x: np.ndarray) -> np.ndarray:
     nan = np.isnan(f)
     r = np.where(nan, (u | 0x400000) & 0xFFFF0000, r)
     return (r.astype(np.uint32)).view(np.float32).astype(np.float64)
-
-
-def round_fp32(x: np.ndarray) -> np.ndarray:
-    return np.asarray(x, dtype=np.float64).astype(np.float32).astype(np.float64)
-
-
-ROUND = {"fp16": round_fp16, "bf16": round_bf16, "fp32": round_fp32}
 
 
 def matmul_f64(a: np.ndarray, b: np.ndarray) -> np.ndarray:

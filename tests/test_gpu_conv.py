@@ -38,6 +38,7 @@ def oracle(x, w, bias):
 
 
 def kernel_for(dtype, B, C, H, W, Co):
+    """Kernel the selector picks for this shape with aligned operands (a prediction)."""
     return cmpext3.plan(dtype, Co, H * W, C, batch=B, has_bias=True).split()[0].split("=")[1]
 
 
@@ -57,6 +58,7 @@ def test_conv2d_1x1_matches_oracle(dtype, shape):
     x, w, bias = make(dtype, B, C, H, W, Co, seed=sum(shape))
     print(f"conv2d {dtype} {shape} kernel={kernel_for(dtype, B, C, H, W, Co)}", flush=True)
     out = cmpext3.conv2d(x.cuda(), w.cuda(), bias.cuda())
+    print(f"  ran: {cmpext3.last_plan()}", flush=True)
     torch.cuda.synchronize()
     assert out.shape == (B, Co, H, W) and out.dtype == DT[dtype] and out.is_contiguous()
     assert O.rel_frobenius(O.to_f64(out.cpu()), oracle(x, w, bias)) <= O.TOLERANCE[dtype]

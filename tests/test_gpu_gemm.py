@@ -36,11 +36,30 @@ def _gpu():
     torch.cuda.init()
 
 
-def note_kernel(dtype, M, N, K, layout="KN", batch=1, has_bias=False, a=None, b=None):
-    desc = cmpext3.plan(dtype, M, N, K, layout=layout, batch=batch, has_bias=has_bias)
-    name = desc.split()[0].split("=")[1]
-    SEEN_KERNELS.add(name)
-    return name
+def kernel_of(desc):
+    return desc.split()[0].split("=")[1]
+
+
+def launched():
+    """(kernel, description) of what the last operator call on this thread ran --
+    its real plan, from the pointers, pitches and workspace of that call."""
+    desc = cmpext3.last_plan()
+    SEEN_KERNELS.add(kernel_of(desc))
+    return kernel_of(desc), desc
+
+
+def cabi_call(dtype, layout, A, lda, stride_a, B, ldb, stride_b, C, ldc, stride_c, bias, M, N, K, batch=1,
+              workspace=None):
+    """cmpext3_gemm_prepare (with the workspace at hand) + cmpext3_gemm_run through the
+    C ABI; returns (status, kernel, description) of the plan that ran."""
+    limit = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    st, call = cabi.prepare(dtype, layout, A, lda, stride_a, B, ldb, stride_b, C, ldc, stride_c, bias, M, N, K,
+                            batch, 0, limit)
+    if st != cabi.OK:
+        return st, None, None
+    _, desc = cabi.describe(call)
+    SEEN_KERNELS.add(kernel_of(desc))
+    return cabi.run(call, workspace), kernel_of(desc), desc
 
 
 def err_vs_oracle(out, a, b, dtype, bias=None, layout="KN"):
@@ -64,8 +83,8 @@ GENERIC_SHAPES = [(1, 1, 1), (3, 5, 7), (65, 33, 17), (100, 7, 33), (129, 257, 6
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("M,N,K", GENERIC_SHAPES)
 def test_generic_ragged(dtype, M, N, K):
-    assert note_kernel(dtype, M, N, K) in ("generic64x64", "skinny")
     a, b, out = run_matmul(dtype, M, N, K, seed=M + N + K)
+    assert launched()[0] in ("generic64x64", "skinny")
     assert err_vs_oracle(out, a, b, dtype) <= O.TOLERANCE[dtype]
 
 
@@ -88,8 +107,9 @@ def test_generic_ragged(dtype, M, N, K):
     (4000, 14000, 520, "tile256x224"),   # ragged 256x224 tiles
 ])
 def test_tiled_shapes(dtype, M, N, K, kernel):
-    assert note_kernel(dtype, M, N, K) == kernel
     a, b, out = run_matmul(dtype, M, N, K, seed=7)
+    name, desc = launched()
+    assert name == kernel, desc
     if M * N * K > 2e9:  # keep the float64 oracle cheap: sampled rows + fp32 GPU reference
         rows = torch.randperm(M, generator=torch.Generator().manual_seed(1))[:96].sort().values
         e = O.rel_frobenius(O.to_f64(out.cpu()[rows]), O.matmul_f64(O.to_f64(a[rows]), O.to_f64(b)))
@@ -107,15 +127,13 @@ def test_tiled_shapes(dtype, M, N, K, kernel):
 def test_skinny(dtype, M, N, K):
     """Binding (wide strips + split K when a workspace helps) and C ABI without
     workspace (narrow strips) both against the oracle."""
-    assert note_kernel(dtype, M, N, K) in ("skinny", "skinny_wide")
     a, b, out = run_matmul(dtype, M, N, K, seed=M)
+    assert launched()[0] in ("skinny", "skinny_wide")
     assert err_vs_oracle(out, a, b, dtype) <= O.TOLERANCE[dtype]
-    kid, desc = cabi.plan(CODE[dtype], cabi.B_KN, M, N, K)          # no workspace
-    name = desc.split()[0].split("=")[1]
-    assert name in ("skinny", "skinny_wide")                        # wide only if it needs no split
-    SEEN_KERNELS.add(name)
     c = torch.empty(M, N, dtype=DT[dtype], device="cuda")
-    assert cabi.matmul(CODE[dtype], a.cuda(), b.cuda(), c, M, N, K) == cabi.OK
+    st, name, desc = cabi_call(CODE[dtype], cabi.B_KN, a.cuda(), K, 0, b.cuda(), N, 0, c, N, 0, None, M, N, K)
+    assert st == cabi.OK and name in ("skinny", "skinny_wide"), desc   # no workspace: wide only unsplit
+    assert "splits=1 " in desc or name == "skinny", desc
     torch.cuda.synchronize()
     assert err_vs_oracle(c, a, b, dtype) <= O.TOLERANCE[dtype]
 
@@ -127,9 +145,9 @@ def test_skinny_split_k_repeated_and_concurrent():
     as the first call, and match the oracle."""
     a, b = O.make_inputs("fp16", 16, 1024, 8192, "normal", 8192 ** -0.5, 3)
     ag, bg = a.cuda(), b.cuda()
-    desc = cmpext3.plan("fp16", 16, 1024, 8192)
-    assert "skinny_wide" in desc and "splits=1 " not in desc, desc
     ref = cmpext3.fp16_matmul(ag, bg)
+    name, desc = launched()
+    assert name == "skinny_wide" and "splits=1 " not in desc, desc
     torch.cuda.synchronize()
     assert err_vs_oracle(ref, a, b, "fp16") <= O.TOLERANCE["fp16"]
     mismatches = torch.zeros((), dtype=torch.int64, device="cuda")
@@ -146,8 +164,9 @@ def test_skinny_split_k_repeated_and_concurrent():
     # batched: every batch entry has its own block of partial sums
     a3 = torch.stack([ag, ag * 0.5, -ag])
     b3 = torch.stack([bg, bg, bg * 2])
-    assert "splits=1 " not in cmpext3.plan("fp16", 16, 1024, 8192, batch=3)
     o3 = cmpext3.bmm(a3, b3)
+    name, desc = launched()
+    assert name == "skinny_wide" and "splits=1 " not in desc, desc
     torch.cuda.synchronize()
     for i in range(3):
         assert err_vs_oracle(o3[i], a3[i], b3[i], "fp16") <= O.TOLERANCE["fp16"]
@@ -177,9 +196,6 @@ def test_split_k_reduction_store_forms(case):
     lay = cabi.B_KN if layout == "KN" else cabi.B_NK
     ldb = N if layout == "KN" else K
     ws_bytes = cabi.workspace_size(CODE[dtype], lay, M, N, K, batch)
-    _, desc = cabi.plan(CODE[dtype], lay, M, N, K, ldc=ldc, has_bias=has_bias, batch=batch,
-                        workspace_bytes=ws_bytes)
-    assert "splits=" in desc and "splits=1 " not in desc, desc
     g = torch.Generator().manual_seed(M + N + K)
     bshape = (K, N) if layout == "KN" else (N, K)
     a = (torch.randn(batch, M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
@@ -190,9 +206,10 @@ def test_split_k_reduction_store_forms(case):
     cbuf = torch.full((stride_c * (batch - 1) + M * ldc + 8,), sentinel, dtype=DT[dtype], device="cuda")
     ws = torch.empty(ws_bytes // 4 + 4, dtype=torch.float32, device="cuda")
     ag, bg = a.cuda(), b.cuda()
-    st = cabi.gemm_ex(CODE[dtype], lay, ag, K, M * K, bg, ldb, K * N, cbuf, ldc, stride_c,
-                      None if bias is None else bias.cuda(), M, N, K, batch, workspace=ws)
+    st, name, desc = cabi_call(CODE[dtype], lay, ag, K, M * K, bg, ldb, K * N, cbuf, ldc, stride_c,
+                               None if bias is None else bias.cuda(), M, N, K, batch, workspace=ws)
     assert st == cabi.OK, cabi.status_string(st)
+    assert "splits=" in desc and "splits=1 " not in desc, desc
     torch.cuda.synchronize()
     cpu = cbuf.cpu()
     written = torch.zeros(cpu.numel(), dtype=torch.bool)
@@ -214,8 +231,9 @@ def test_split_k_reduction_store_forms(case):
                                           (301, 257, 777, "f32tile64x64k4"),
                                           (1440, 768, 200, "f32tile96x64"), (1439, 767, 201, "f32tile96x64")])
 def test_fp32(M, N, K, kernel):
-    assert note_kernel("fp32", M, N, K) == kernel
     a, b, out = run_matmul("fp32", M, N, K, seed=3, dist="uniform")
+    name, desc = launched()
+    assert name == kernel, desc
     assert err_vs_oracle(out, a, b, "fp32") <= O.TOLERANCE["fp32"]
 
 
@@ -271,7 +289,9 @@ def test_linear_with_bias(dtype, shape):
     out = cmpext3.linear(x.cuda(), w.cuda(), bias.cuda())
     torch.cuda.synchronize()
     assert out.shape == (Bt, S, N)
-    note_kernel(dtype, Bt * S, N, K, layout="NK", has_bias=True)
+    name, desc = launched()
+    if shape == (1, 512, 7168, 7168) and dtype != "fp32":  # the binding's workspace: 256x224 tiles split K
+        assert name == "tile256x224" and "splits=4" in desc, desc
     ref = O.linear_f64(O.to_f64(x), O.to_f64(w), O.to_f64(bias))
     assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
     out_nb = cmpext3.linear(x.cuda(), w.cuda())
@@ -288,11 +308,10 @@ def test_skinny_linear_weight_binding_and_c_abi(dtype):
     w = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(DT[dtype])
     ref = O.linear_f64(O.to_f64(x), O.to_f64(w))
     out = cmpext3.linear(x.cuda(), w.cuda())
-    kid, desc = cabi.plan(CODE[dtype], cabi.B_NK, M, N, K)
-    assert "skinny_nk" in desc, desc
-    SEEN_KERNELS.add("skinny_nk")
+    assert launched()[0] == "skinny_nk"
     c = torch.empty(M, N, dtype=DT[dtype], device="cuda")
-    assert cabi.gemm_ex(CODE[dtype], cabi.B_NK, x.cuda(), K, 0, w.cuda(), K, 0, c, N, 0, None, M, N, K) == cabi.OK
+    st, name, _ = cabi_call(CODE[dtype], cabi.B_NK, x.cuda(), K, 0, w.cuda(), K, 0, c, N, 0, None, M, N, K)
+    assert st == cabi.OK and name == "skinny_nk"
     torch.cuda.synchronize()
     assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
     assert torch.equal(out, c)
@@ -307,11 +326,10 @@ def test_weight_layout_batched_and_bias_c_abi(dtype):
     Bn, M, N, K = 3, 16, 1000, 520
     a = (torch.randn(Bn, M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
     w = (torch.randn(Bn, N, K, generator=g) / np.sqrt(K)).to(DT[dtype])
-    assert "skinny_nk" in cmpext3.plan(dtype, M, N, K, layout="NK", batch=Bn)
     ag, wg = a.cuda(), w.cuda()
     c = torch.empty(Bn, M, N, dtype=DT[dtype], device="cuda")
-    st = cabi.gemm_ex(CODE[dtype], cabi.B_NK, ag, K, M * K, wg, K, N * K, c, N, M * N, None, M, N, K, Bn)
-    assert st == cabi.OK
+    st, name, _ = cabi_call(CODE[dtype], cabi.B_NK, ag, K, M * K, wg, K, N * K, c, N, M * N, None, M, N, K, Bn)
+    assert st == cabi.OK and name == "skinny_nk"
     for i in range(Bn):
         ci = torch.empty(M, N, dtype=DT[dtype], device="cuda")
         assert cabi.gemm_ex(CODE[dtype], cabi.B_NK, ag[i], K, 0, wg[i], K, 0, ci, N, 0, None, M, N, K) == cabi.OK
@@ -323,9 +341,8 @@ def test_weight_layout_batched_and_bias_c_abi(dtype):
     x = (torch.randn(M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
     w2 = (torch.randn(N, K, generator=g) / np.sqrt(K)).to(DT[dtype])
     bias = torch.randn(N, generator=g).to(DT[dtype])
-    assert "tile64x256" in cmpext3.plan(dtype, M, N, K, layout="NK", has_bias=True)
-    SEEN_KERNELS.add("tile64x256")
     out = cmpext3.linear(x.cuda(), w2.cuda(), bias.cuda())
+    assert launched()[0] == "tile64x256"
     torch.cuda.synchronize()
     ref = O.linear_f64(O.to_f64(x), O.to_f64(w2), O.to_f64(bias))
     assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
@@ -341,11 +358,12 @@ def test_unaligned_operands_padded(dtype):
     for M, N, K in [(1023, 1025, 1027), (1024, 1031, 1024), (640, 1024, 1001)]:
         a = (torch.randn(M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
         b = (torch.randn(K, N, generator=g)).to(DT[dtype])
-        desc = cmpext3.plan(dtype, M, N, K)
-        assert "padded=" in desc and "generic" not in desc, desc
         out = MATMUL[dtype](a.cuda(), b.cuda())
+        name, desc = launched()
+        assert "padded=" in desc and name != "generic64x64", desc
         c = torch.empty(M, N, dtype=DT[dtype], device="cuda")
-        assert cabi.gemm_ex(CODE[dtype], cabi.B_KN, a.cuda(), K, 0, b.cuda(), N, 0, c, N, 0, None, M, N, K) == cabi.OK
+        st, name, _ = cabi_call(CODE[dtype], cabi.B_KN, a.cuda(), K, 0, b.cuda(), N, 0, c, N, 0, None, M, N, K)
+        assert st == cabi.OK and name == "generic64x64"   # no workspace: element loads
         torch.cuda.synchronize()
         ref = O.matmul_f64(O.to_f64(a), O.to_f64(b))
         assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
@@ -355,18 +373,22 @@ def test_unaligned_operands_padded(dtype):
     w = (torch.randn(1999, 1001, generator=g) / 32).to(DT[dtype])
     bias = torch.randn(1999, generator=g).to(DT[dtype])
     out = cmpext3.linear(x.cuda(), w.cuda(), bias.cuda())
+    name, desc = launched()
+    assert name == "tile128x128" and "padded=AB" in desc, desc
     ref = O.linear_f64(O.to_f64(x), O.to_f64(w), O.to_f64(bias))
     assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
     base = (torch.randn(1025, 1025, generator=g) / 32).to(DT[dtype])
     b2 = (torch.randn(1024, 768, generator=g) / 32).to(DT[dtype])
-    view = base.cuda()[1:, 1:]  # rows start 2 bytes off 16-byte alignment (generic kernel: no padded workspace)
+    view = base.cuda()[1:, 1:]  # rows start 2 bytes off 16-byte alignment: A is copied zero-padded
     out = MATMUL[dtype](view, b2.cuda())
+    name, desc = launched()
+    assert "padded=A" in desc and name != "generic64x64", desc
     ref = O.matmul_f64(O.to_f64(base[1:, 1:]), O.to_f64(b2))
     assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
     a3 = (torch.randn(3, 300, 257, generator=g) / 16).to(DT[dtype])
     b3 = (torch.randn(3, 257, 301, generator=g) / 16).to(DT[dtype])
-    assert "padded=AB" in cmpext3.plan(dtype, 300, 301, 257, batch=3)
     out = cmpext3.bmm(a3.cuda(), b3.cuda())
+    assert "padded=AB" in launched()[1]
     torch.cuda.synchronize()
     for i in range(3):
         ref = O.matmul_f64(O.to_f64(a3[i]), O.to_f64(b3[i]))
@@ -381,12 +403,12 @@ def test_fp32_dma16(M, N, K, kernel, layout):
     """fp32 operands with 16-byte aligned rows and K, N multiples of 4 load through
     16-byte LDS-DMA: every tile, both B layouts, M/N tails, K % 16 != 0 and K splits
     (520 x 516 x 1028 on 64x64k4)."""
-    desc = cmpext3.plan("fp32", M, N, K, layout=layout)
-    assert "dma16" in desc and note_kernel("fp32", M, N, K, layout=layout) == kernel, desc
     g = torch.Generator().manual_seed(M + K)
     a = torch.rand(M, K, generator=g) * 2 - 1
     b = torch.rand(K, N, generator=g) * 2 - 1 if layout == "KN" else torch.rand(N, K, generator=g) * 2 - 1
     out = cmpext3.fp32_matmul(a.cuda(), b.cuda()) if layout == "KN" else cmpext3.linear(a.cuda(), b.cuda())
+    name, desc = launched()
+    assert "dma16" in desc and name == kernel, desc
     torch.cuda.synchronize()
     assert err_vs_oracle(out, a, b, "fp32", layout=layout) <= O.TOLERANCE["fp32"]
     if layout == "KN":  # a view whose rows start 4 bytes in takes the 4-byte path
@@ -411,22 +433,22 @@ def test_fp32_unaligned_padded():
     than the copies cost), against the oracle."""
     g = torch.Generator().manual_seed(41)
     for M, N, K in [(2049, 2999, 3001), (2500, 2501, 2502)]:
-        desc = cmpext3.plan("fp32", M, N, K)
-        assert "padded=AB" in desc and "dma16" in desc, desc
-        assert "padded" not in cabi.plan(cabi.F32, cabi.B_KN, M, N, K)[1]
         a = torch.rand(M, K, generator=g) * 2 - 1
         b = torch.rand(K, N, generator=g) * 2 - 1
         out = cmpext3.fp32_matmul(a.cuda(), b.cuda())
+        name, desc = launched()
+        assert "padded=AB" in desc and "dma16" in desc, desc
         c = torch.empty(M, N, device="cuda")
-        assert cabi.gemm_ex(cabi.F32, cabi.B_KN, a.cuda(), K, 0, b.cuda(), N, 0, c, N, 0, None, M, N, K) == cabi.OK
+        st, name, desc = cabi_call(cabi.F32, cabi.B_KN, a.cuda(), K, 0, b.cuda(), N, 0, c, N, 0, None, M, N, K)
+        assert st == cabi.OK and "padded" not in desc, desc
         torch.cuda.synchronize()
         assert err_vs_oracle(out, a, b, "fp32") <= O.TOLERANCE["fp32"]
         assert torch.equal(out, c)
     x = torch.rand(2049, 3001, generator=g) * 2 - 1
     w = torch.rand(2999, 3001, generator=g) * 2 - 1
     bias = torch.rand(2999, generator=g)
-    assert "padded=AB" in cmpext3.plan("fp32", 2049, 2999, 3001, layout="NK", has_bias=True)
     out = cmpext3.linear(x.cuda(), w.cuda(), bias.cuda())
+    assert "padded=AB" in launched()[1]
     ref = O.linear_f64(O.to_f64(x), O.to_f64(w), O.to_f64(bias))
     assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE["fp32"]
     a3 = torch.rand(2, 1537, 2003, generator=g) * 2 - 1
@@ -443,25 +465,27 @@ def test_fp32_m16_tile():
     workgroups, Linear (W as [N, K]) with bias, and a batch, against the oracle."""
     g = torch.Generator().manual_seed(61)
     for M, N, K in [(13, 1001, 333), (7, 3000, 777), (16, 1000, 100), (16, 4096, 4096)]:
-        assert note_kernel("fp32", M, N, K) == "f32tile16x64k4", cmpext3.plan("fp32", M, N, K)
         a = torch.rand(M, K, generator=g) * 2 - 1
         b = torch.rand(K, N, generator=g) * 2 - 1
         out = cmpext3.fp32_matmul(a.cuda(), b.cuda())
+        name, desc = launched()
+        assert name == "f32tile16x64k4", desc
+        if (M, N, K) == (16, 4096, 4096):
+            assert "splits=" in desc, desc
         torch.cuda.synchronize()
         assert err_vs_oracle(out, a, b, "fp32") <= O.TOLERANCE["fp32"]
-    assert "splits=" in cmpext3.plan("fp32", 16, 4096, 4096)
     for M, N, K in [(5, 1000, 1000), (16, 4096, 4096)]:
         x = torch.rand(M, K, generator=g) * 2 - 1
         w = torch.rand(N, K, generator=g) * 2 - 1
         bias = torch.rand(N, generator=g)
-        assert note_kernel("fp32", M, N, K, layout="NK", has_bias=True) == "f32tile16x64k4"
         out = cmpext3.linear(x.cuda(), w.cuda(), bias.cuda())
+        assert launched()[0] == "f32tile16x64k4"
         ref = O.linear_f64(O.to_f64(x), O.to_f64(w), O.to_f64(bias))
         assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE["fp32"]
     a3 = torch.rand(4, 16, 1000, generator=g) * 2 - 1
     b3 = torch.rand(4, 1000, 512, generator=g) * 2 - 1
-    assert note_kernel("fp32", 16, 512, 1000, batch=4) == "f32tile16x64k4"
     out = cmpext3.bmm(a3.cuda(), b3.cuda())
+    assert launched()[0] == "f32tile16x64k4"
     torch.cuda.synchronize()
     for i in range(4):
         assert err_vs_oracle(out[i], a3[i], b3[i], "fp32") <= O.TOLERANCE["fp32"]
@@ -473,23 +497,23 @@ def test_fp32_split_k():
     and a batch, against the oracle at fp32's 1e-5."""
     g = torch.Generator().manual_seed(31)
     for M, N, K in [(16, 1024, 14336), (130, 1000, 4100)]:
-        assert "splits=" in cmpext3.plan("fp32", M, N, K), cmpext3.plan("fp32", M, N, K)
         a = torch.rand(M, K, generator=g) * 2 - 1
         b = torch.rand(K, N, generator=g) * 2 - 1
         out = cmpext3.fp32_matmul(a.cuda(), b.cuda())
+        assert "splits=" in launched()[1]
         torch.cuda.synchronize()
         assert err_vs_oracle(out, a, b, "fp32") <= O.TOLERANCE["fp32"]
     x = torch.rand(64, 8192, generator=g) * 2 - 1
     w = torch.rand(512, 8192, generator=g) * 2 - 1
     bias = torch.rand(512, generator=g)
-    assert "splits=" in cmpext3.plan("fp32", 64, 512, 8192, layout="NK", has_bias=True)
     out = cmpext3.linear(x.cuda(), w.cuda(), bias.cuda())
+    assert "splits=" in launched()[1]                 # linear passes its workspace: K splits
     ref = O.linear_f64(O.to_f64(x), O.to_f64(w), O.to_f64(bias))
     assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE["fp32"]
     a3 = torch.rand(3, 64, 4096, generator=g) * 2 - 1
     b3 = torch.rand(3, 4096, 256, generator=g) * 2 - 1
-    assert "splits=" in cmpext3.plan("fp32", 64, 256, 4096, batch=3)
     out = cmpext3.bmm(a3.cuda(), b3.cuda())
+    assert "splits=" in launched()[1]
     torch.cuda.synchronize()
     for i in range(3):
         assert err_vs_oracle(out[i], a3[i], b3[i], "fp32") <= O.TOLERANCE["fp32"]
@@ -520,12 +544,12 @@ def test_bmm(dtype, Bn, M, N, K):
     b = (torch.randn(Bn, K, N, generator=g) / np.sqrt(K)).to(DT[dtype])
     out = cmpext3.bmm(a.cuda(), b.cuda())
     torch.cuda.synchronize()
-    note_kernel(dtype, M, N, K, batch=Bn)
+    _, desc_b = launched()
     ref = O.bmm_f64(O.to_f64(a), O.to_f64(b))
     assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
-    for i in range(Bn):  # each batch entry equals the 2-D op on its slice, bit for bit
+    for i in range(Bn):  # each batch entry equals the 2-D op on its slice, bit for bit, on the same plan
         single = MATMUL[dtype](a[i].cuda(), b[i].cuda())
-        if cmpext3.plan(dtype, M, N, K) == cmpext3.plan(dtype, M, N, K, batch=Bn).replace(f"x{Bn} ", "x1 "):
+        if launched()[1] == desc_b.replace(f"x{Bn} ", "x1 "):
             assert torch.equal(single, out[i])
 
 
@@ -588,14 +612,15 @@ def _full_config_check(name, via_cabi=False):
     dtype, M, N, K = c["dtype"], c["M"], c["N"], c["K"]
     a, b = O.make_inputs(dtype, M, N, K, c["dist"], c.get("scale", 1.0), 0)
     ag, bg = a.cuda(), b.cuda()
-    note_kernel(dtype, M, N, K)
     out = MATMUL[dtype](ag, bg)
+    _, desc = launched()
     if via_cabi:
         # same kernel through the C ABI (with the workspace the binding uses): bit-identical
         c2 = torch.empty_like(out)
         ws_bytes = cabi.workspace_size(CODE[dtype], cabi.B_KN, M, N, K)
         ws = torch.empty(max(ws_bytes, 0), dtype=torch.uint8, device="cuda") if ws_bytes > 0 else None
-        assert cabi.gemm_ex(CODE[dtype], cabi.B_KN, ag, K, 0, bg, N, 0, c2, N, 0, None, M, N, K, 1, ws) == cabi.OK
+        st, _, desc2 = cabi_call(CODE[dtype], cabi.B_KN, ag, K, 0, bg, N, 0, c2, N, 0, None, M, N, K, 1, ws)
+        assert st == cabi.OK and desc2 == desc, (desc, desc2)
         torch.cuda.synchronize()
         assert torch.equal(out, c2)
         # the reference-shaped entry point (no workspace) within tolerance
@@ -651,6 +676,59 @@ def test_cfg4_fp16_skinny():
 
 def test_cfg5_fp32_ragged():
     _full_config_check("cfg5_fp32_ragged", via_cabi=True)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_linear_misaligned_bias_stays_tiled(dtype):
+    """A bias view that is only 2-byte aligned (bias[1:]) is read element by element
+    in the epilogue; the product stays on the tiled kernel and gives the same bits as
+    an aligned copy of the same bias.  Against the float64 oracle on sampled rows."""
+    M = N = K = 4096
+    g = torch.Generator().manual_seed(77)
+    x = (torch.randn(M, K, generator=g) / 8).to(DT[dtype]).cuda()
+    w = (torch.randn(N, K, generator=g) / 8).to(DT[dtype]).cuda()
+    bias_full = torch.randn(N + 1, generator=g).to(DT[dtype]).cuda()
+    bias_view = bias_full[1:]
+    assert bias_view.data_ptr() % 8 == 2
+    out = cmpext3.linear(x, w, bias_view)
+    name, desc = launched()
+    assert name == "tile256x256", desc
+    out_aligned = cmpext3.linear(x, w, bias_view.clone())
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_aligned)
+    rows = [0, 1, 1000, 4095]
+    ref = O.linear_f64(O.to_f64(x[rows].cpu()), O.to_f64(w.cpu()), O.to_f64(bias_view.cpu()))
+    assert O.rel_frobenius(O.to_f64(out[rows].cpu()), ref) <= O.TOLERANCE[dtype]
+    # the ragged tail (N % 4 != 0) with a misaligned bias, 128x128 tiles
+    x2, w2 = x[:1000, :1000].contiguous(), w[:1002, :1000].contiguous()
+    b2 = bias_full[1:1003]
+    out2 = cmpext3.linear(x2, w2, b2)
+    torch.cuda.synchronize()
+    assert launched()[0] != "generic64x64"
+    ref2 = O.linear_f64(O.to_f64(x2.cpu()), O.to_f64(w2.cpu()), O.to_f64(b2.cpu()))
+    assert O.rel_frobenius(O.to_f64(out2.cpu()), ref2) <= O.TOLERANCE[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_tiled_split_k_batched(dtype):
+    """16-bit tiled products that split K inside a batch (grid.z = batch * splits):
+    bmm of 3 x 256x4096x4096, every batch entry against the float64 oracle, and
+    equal bit for bit to the same entry computed alone (same tile and split)."""
+    Bn, M, N, K = 3, 256, 4096, 4096
+    g = torch.Generator().manual_seed(88)
+    a = (torch.randn(Bn, M, K, generator=g) / 64).to(DT[dtype])
+    b = (torch.randn(Bn, K, N, generator=g) / 64).to(DT[dtype])
+    out = cmpext3.bmm(a.cuda(), b.cuda())
+    name, desc = launched()
+    assert name.startswith("tile") and "splits=" in desc and "splits=1 " not in desc, desc
+    torch.cuda.synchronize()
+    for i in range(Bn):
+        ref = O.matmul_f64(O.to_f64(a[i]), O.to_f64(b[i]))
+        assert O.rel_frobenius(O.to_f64(out[i].cpu()), ref) <= O.TOLERANCE[dtype], i
+    single = cmpext3.bmm(a[1:2].cuda(), b[1:2].cuda())
+    _, desc1 = launched()
+    if desc1.split()[0] == desc.split()[0] and desc1.split("splits=")[1].split()[0] == desc.split("splits=")[1].split()[0]:
+        assert torch.equal(single[0], out[1])
 
 
 def test_every_kernel_family_was_exercised():

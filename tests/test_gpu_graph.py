@@ -53,10 +53,16 @@ def _calls(t):
     ]
 
 
-def test_plans_cover_the_paths():
-    assert "splits=" in cmpext3.plan("fp16", 16, 1024, 8192)
-    assert "padded=" in cmpext3.plan("fp32", 2049, 2999, 3001)
-    assert "k4" in cmpext3.plan("fp32", 300, 1000, 1000, layout="NK", has_bias=True)
+def test_calls_cover_the_paths():
+    t = _inputs()
+    ran = []
+    for f in _calls(t):
+        f()
+        ran.append(cmpext3.last_plan())
+    torch.cuda.synchronize()
+    assert "splits=" in ran[1] and "splits=1 " not in ran[1], ran[1]
+    assert "padded=" in ran[2], ran[2]
+    assert "k4" in ran[3], ran[3]
 
 
 def test_graph_replays_match_eager():

@@ -292,3 +292,115 @@ def test_conv_planted_mistakes_are_caught(golden, mutant):
     x, w, bias, exp = conv_operands(golden, "conv_f16_2x5x3x4_o6_bias")
     out = mutant(x, w, bias)
     assert out.shape != exp.shape or O.rel_frobenius(out, exp) > O.TOLERANCE["fp16"]
+
+
+# ---- the seeded input generator against the distributions BASELINE.json names ----
+
+def _sample(t, n=200_000):
+    """Up to n values of a tensor as float64 (a fixed stride through it)."""
+    v = O.to_f64(t).reshape(-1)
+    return v[:: max(1, v.size // n)][:n]
+
+
+def distribution_ok(t, dist, scale=1.0, alpha=1e-4):
+    """True when the values of t look like iid draws of the named distribution:
+    Kolmogorov-Smirnov against scipy's CDF, plus range (uniform), mean and spread
+    within a few standard errors of the distribution's own."""
+    from scipy import stats
+
+    v = _sample(t)
+    n = v.size
+    if dist == "uniform":
+        if v.min() < -1.0 or v.max() > 1.0:
+            return False
+        sd = math.sqrt(1.0 / 3.0)
+        if stats.kstest(v, "uniform", args=(-1.0, 2.0)).pvalue < alpha:
+            return False
+    else:
+        sd = scale
+        if stats.kstest(v, "norm", args=(0.0, scale)).pvalue < alpha:
+            return False
+    if abs(v.mean()) > 5 * sd / math.sqrt(n):
+        return False
+    # the sample variance of n iid draws has a relative standard error of about sqrt(2/n)
+    # (normal; smaller for uniform)
+    return abs(v.var() / sd ** 2 - 1.0) < 6 * math.sqrt(2.0 / n)
+
+
+def independent(a, b):
+    """A and B are distinct draws: not equal and uncorrelated (|r| < 5 / sqrt(n))."""
+    x, y = _sample(a), _sample(b)
+    n = min(x.size, y.size)
+    x, y = x[:n], y[:n]
+    if np.array_equal(x, y):
+        return False
+    return abs(np.corrcoef(x, y)[0, 1]) < 5 / math.sqrt(n)
+
+
+@pytest.mark.parametrize("cname", sorted(O.CONFIGS))
+def test_make_inputs_follows_the_config_distributions(cname):
+    c = O.CONFIGS[cname]
+    # the full shapes, but small M keeps it quick: B is drawn whole
+    M = min(c["M"], 64)
+    a, b = O.make_inputs(c["dtype"], M, c["N"], c["K"], c["dist"], c.get("scale", 1.0), 0)
+    tdt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[c["dtype"]]
+    assert a.dtype == tdt and b.dtype == tdt and a.shape == (M, c["K"]) and b.shape == (c["K"], c["N"])
+    assert distribution_ok(a, c["dist"], c.get("scale", 1.0)), cname
+    assert distribution_ok(b, c["dist"], c.get("scale", 1.0)), cname
+    assert independent(a, b)
+
+
+def test_make_inputs_scales_are_the_configs():
+    # BASELINE.json: N(0,1)/sqrt(4096), N(0,0.02), N(0,1)/sqrt(8192), U[-1,1] for fp32
+    assert O.CONFIGS["cfg2_fp16_4096"]["scale"] == 1 / 64
+    assert O.CONFIGS["cfg3_bf16_mlp"]["scale"] == 0.02
+    assert math.isclose(O.CONFIGS["cfg4_fp16_skinny"]["scale"], 1 / math.sqrt(8192), rel_tol=1e-15)
+    assert O.CONFIGS["cfg1_fp32_512"]["dist"] == O.CONFIGS["cfg5_fp32_ragged"]["dist"] == "uniform"
+
+
+def test_make_inputs_draw_order_and_seeding():
+    # A is drawn first: it does not depend on N (nor on B's layout); B continues the same
+    # stream, so it moves with the size of A; another seed moves both; same seed, same bits
+    a1, b1 = O.make_inputs("fp32", 8, 40, 16, "uniform", 1.0, 3)
+    a2, b2 = O.make_inputs("fp32", 8, 24, 16, "uniform", 1.0, 3)
+    a3, b3 = O.make_inputs("fp32", 9, 40, 16, "uniform", 1.0, 3)
+    a4, b4 = O.make_inputs("fp32", 8, 40, 16, "uniform", 1.0, 4)
+    a5, b5 = O.make_inputs("fp32", 8, 40, 16, "uniform", 1.0, 3, b_layout="NK")
+    assert torch.equal(a1, a2) and torch.equal(a1, a5) and torch.equal(a1, a3[:8])
+    # B starts where A ends in the stream, whatever N is: the smaller B is a prefix
+    assert torch.equal(b1.reshape(-1)[:16 * 24], b2.reshape(-1))
+    assert not torch.equal(b1, b3) and not torch.equal(a1, a4) and not torch.equal(b1, b4)
+    assert b5.shape == (40, 16) and torch.equal(b5.reshape(-1), b1.reshape(-1))
+    a6, b6 = O.make_inputs("fp32", 8, 40, 16, "uniform", 1.0, 3)
+    assert torch.equal(a1, a6) and torch.equal(b1, b6)
+    # values are representable in the dtype (cast once, no further rounding)
+    a7, b7 = O.make_inputs("fp16", 64, 64, 64, "normal", 0.1, 0)
+    assert np.array_equal(O.round_fp16(O.to_f64(a7)), O.to_f64(a7))
+    a8, _ = O.make_inputs("bf16", 64, 64, 64, "normal", 0.1, 0)
+    assert np.array_equal(O.round_bf16(O.to_f64(a8)), O.to_f64(a8))
+
+
+def _mutant_inputs(kind, M, N, K, dist, scale, seed):
+    """make_inputs with one plausible mistake (for the planted-mistake check)."""
+    g = torch.Generator().manual_seed(seed)
+    if kind == "rand_for_randn":
+        return torch.rand((M, K), generator=g) * scale, torch.rand((K, N), generator=g) * scale
+    if kind == "wrong_scale":
+        return torch.randn((M, K), generator=g) * scale * 1.25, torch.randn((K, N), generator=g) * scale * 1.25
+    if kind == "unit_range":
+        return torch.rand((M, K), generator=g), torch.rand((K, N), generator=g)
+    if kind == "half_range":
+        return torch.rand((M, K), generator=g) - 0.5, torch.rand((K, N), generator=g) - 0.5
+    if kind == "b_equals_a":
+        a = torch.randn((M, K), generator=g) * scale
+        return a, a.clone().reshape(K, N)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind,dist", [("rand_for_randn", "normal"), ("wrong_scale", "normal"),
+                                       ("unit_range", "uniform"), ("half_range", "uniform"),
+                                       ("b_equals_a", "normal")])
+def test_make_inputs_checks_catch_planted_mistakes(kind, dist):
+    a, b = _mutant_inputs(kind, 256, 256, 256, dist, 0.02, 0)
+    ok = distribution_ok(a, dist, 0.02) and distribution_ok(b, dist, 0.02) and independent(a, b)
+    assert not ok, kind
