@@ -135,7 +135,10 @@ class PowerClock:
         if not clks and num(m.get("current_gfxclk")):
             clks = [num(m.get("current_gfxclk"))]
         return {"power_w": num(m.get("current_socket_power")) or num(m.get("average_socket_power")),
-                "clks": clks, "stamp": m.get("firmware_timestamp"), "t": time.perf_counter()}
+                "clks": clks, "stamp": m.get("firmware_timestamp"), "t": time.perf_counter(),
+                "throttle": m.get("indep_throttle_status"),
+                "acc": {k: m.get(k) for k in ("accumulation_counter", "ppt_residency_acc", "socket_thm_residency_acc",
+                                              "vr_thm_residency_acc", "hbm_thm_residency_acc", "prochot_residency_acc")}}
 
     def sample_until(self, event, deadline: float, out: list) -> None:
         """Read samples into `out` while `event` (a recorded torch event) is pending
@@ -163,6 +166,20 @@ class PowerClock:
         if not fresh:
             return {"samples": 0, "reads": len(samples),
                     "error": "the firmware's metrics table did not refresh during the window"}
+        # how much of the window each limiter was engaged: residency counters advance with the
+        # firmware's accumulation counter while that limit holds the clock down
+        first, last = fresh[0]["acc"], fresh[-1]["acc"]
+        limits = {}
+        try:
+            ticks = last["accumulation_counter"] - first["accumulation_counter"]
+            if ticks > 0:
+                for k in ("ppt_residency_acc", "socket_thm_residency_acc", "vr_thm_residency_acc",
+                          "hbm_thm_residency_acc", "prochot_residency_acc"):
+                    if isinstance(first.get(k), int) and isinstance(last.get(k), int):
+                        limits[k.replace("_residency_acc", "")] = round((last[k] - first[k]) / ticks, 3)
+        except (TypeError, KeyError):
+            limits = {}
+        throttle = sorted({str(x["throttle"]) for x in fresh if x["throttle"] not in (None, "N/A")})
         samples = fresh
         pw = [x["power_w"] for x in samples if x["power_w"]]
         clk = [sum(x["clks"]) / len(x["clks"]) for x in samples if x["clks"]]
@@ -173,6 +190,7 @@ class PowerClock:
                 "avg_sclk_mhz": round(statistics.mean(clk), 1) if clk else None,
                 "xcd_sclk_mhz_range": [round(min(lo)), round(max(hi))] if lo else None,
                 "window_s": round(window_s, 3),
+                "limit_residency": limits or None, "throttle_status": throttle or None,
                 "source": "amdsmi gpu_metrics (current_socket_power; current_gfxclks averaged over the XCDs), "
                           "one sample per firmware refresh, read while the same op ran back to back for "
                           "window_s right after its timed steps"}
@@ -191,29 +209,16 @@ def power_clock() -> PowerClock:
 POWER_WINDOW_S = 1.0
 
 
-def set_power_window(seconds: float) -> None:
-    global POWER_WINDOW_S
-    POWER_WINDOW_S = seconds
-
-
-def timed_region(fn, steps: int, warmup: int, power_window_s: float | None = None) -> tuple[float, float, dict]:
+def timed_region(fn, steps: int, warmup: int) -> tuple[float, float]:
     """W untimed calls, then K calls between two events on the current stream
-    (the stream the kernels run on), bracketed by synchronizations.  Then, outside
-    the timed region, the same call back to back for `power_window_s` seconds while
-    board power and shader clock are read (the timed steps are too short for the
-    firmware's metrics to refresh inside them).  Returns (wall ms per step, event
-    ms per step, power/clock summary)."""
+    (the stream the kernels run on), bracketed by synchronizations.  Returns
+    (wall ms per step, event ms per step)."""
     import torch
 
     stream = torch.cuda.current_stream()
-    marks = [torch.cuda.Event(enable_timing=True) for _ in range(warmup + 1)]
-    marks[0].record(stream)
     for i in range(warmup):
         fn(i)
-        marks[i + 1].record(stream)
     torch.cuda.synchronize()
-    # the GPU time of one step, from the warm-up calls (median: the first may load code)
-    est_ms = statistics.median(marks[i].elapsed_time(marks[i + 1]) for i in range(warmup)) if warmup else 0.0
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
@@ -222,29 +227,36 @@ def timed_region(fn, steps: int, warmup: int, power_window_s: float | None = Non
     e1.record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    wall_ms, kern_ms = (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
-    window = POWER_WINDOW_S if power_window_s is None else power_window_s
-    samples = []
+    return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
+
+
+def power_window(fn, kern_ms: float, window_s: float) -> dict:
+    """The call back to back for `window_s` seconds while board power, shader clock and
+    the firmware's limiter residencies are read (a timed region of a few ms is too
+    short for the firmware's metrics table to refresh inside it).  Run after every
+    workload's timed steps, so that its heat does not shape the next timed region."""
+    import torch
+
     pc = power_clock()
-    if window > 0 and pc.handle is not None:
-        # batches of ~20 ms, two in flight, so the GPU never idles while the host reads
-        per = max(1, int(20.0 / max(kern_ms, 1e-3)))
-        pending = []
-        w0 = time.perf_counter()
-        i = 0
-        while time.perf_counter() - w0 < window or pending:
-            if time.perf_counter() - w0 < window:
-                for _ in range(per):
-                    fn(i)
-                    i += 1
-                ev = torch.cuda.Event()
-                ev.record(stream)
-                pending.append(ev)
-            if len(pending) >= 2 or time.perf_counter() - w0 >= window:
-                pc.sample_until(pending.pop(0), float("inf"), samples)
-        torch.cuda.synchronize()
-        window = time.perf_counter() - w0
-    return wall_ms, kern_ms, pc.summary(samples, window)
+    if window_s <= 0 or pc.handle is None:
+        return pc.summary([], 0.0) if pc.handle is None else {"samples": 0, "error": "window disabled"}
+    stream = torch.cuda.current_stream()
+    samples, pending = [], []
+    per = max(1, int(20.0 / max(kern_ms, 1e-3)))  # batches of ~20 ms, two in flight
+    w0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - w0 < window_s or pending:
+        if time.perf_counter() - w0 < window_s:
+            for _ in range(per):
+                fn(i)
+                i += 1
+            ev = torch.cuda.Event()
+            ev.record(stream)
+            pending.append(ev)
+        if len(pending) >= 2 or time.perf_counter() - w0 >= window_s:
+            pc.sample_until(pending.pop(0), float("inf"), samples)
+    torch.cuda.synchronize()
+    return pc.summary(samples, time.perf_counter() - w0)
 
 
 def make_gpu_inputs(c, nb: int, seed: int = 0):
@@ -274,19 +286,19 @@ def time_gpu(name: str, steps: int, warmup: int, with_torch: bool = True) -> dic
     # Infinity Cache across calls, so it cycles through 4 distinct B buffers.
     nb = 4 if c.get("hbm") else 1
     a, bs = make_gpu_inputs(c, nb)
-    wall_ms, kern_ms, pwr = timed_region(lambda i: fn(a, bs[i % nb]), steps, warmup)
+    wall_ms, kern_ms = timed_region(lambda i: fn(a, bs[i % nb]), steps, warmup)
     plan = cmpext3.last_plan()
     flops, nbytes = algorithmic(c)
     r = dict(config=name, desc=c["desc"], dtype=c["dtype"], kernel=plan.split()[0].split("=")[1], plan=plan,
-             power=pwr, ms_per_step=wall_ms, kernel_ms=kern_ms,
+             power=None, ms_per_step=wall_ms, kernel_ms=kern_ms,
              tflops=flops / (wall_ms * 1e-3) / 1e12, kernel_tflops=flops / (kern_ms * 1e-3) / 1e12,
              gbs=nbytes / (wall_ms * 1e-3) / 1e9, kernel_gbs=nbytes / (kern_ms * 1e-3) / 1e9)
     if with_torch:
         t = torch_same_device(torch.matmul, lambda i: (a, bs[i % nb]), steps, warmup, flops, nbytes, c.get("hbm"))
         t["speedup"] = round(t["kernel_ms"] / kern_ms, 3)
         r["torch_same_device"] = t
-    del a, bs
-    torch.cuda.empty_cache()
+    # run later (power_window), after every workload's timed steps; keeps the inputs alive
+    r["power_job"] = lambda window_s: power_window(lambda i: fn(a, bs[i % nb]), kern_ms, window_s)
     return r
 
 
@@ -340,7 +352,7 @@ def time_caller(name: str, steps: int, warmup: int, with_torch: bool = True) -> 
     c = CALLERS[name]
     args = caller_inputs(c, "cuda")
     fn = caller_fn(c, cmpext3)
-    wall_ms, kern_ms, pwr = timed_region(lambda i: fn(*args), steps, warmup)
+    wall_ms, kern_ms = timed_region(lambda i: fn(*args), steps, warmup)
     flops, nbytes = caller_algorithmic(c)
     plan = cmpext3.last_plan()
     kernel = plan.split()[0].split("=")[1]
@@ -349,8 +361,6 @@ def time_caller(name: str, steps: int, warmup: int, with_torch: bool = True) -> 
         tfn = {"linear": F.linear, "bmm": torch.bmm, "conv": F.conv2d}[c["op"]]
         ref = torch_same_device(tfn, lambda i: args, steps, warmup, flops, nbytes, c.get("hbm"))
         ref["speedup"] = round(ref["kernel_ms"] / kern_ms, 3)
-    del args
-    torch.cuda.empty_cache()
     if c.get("hbm"):
         ach, peak, unit, bound = nbytes / (kern_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", "hbm"
     else:
@@ -360,8 +370,9 @@ def time_caller(name: str, steps: int, warmup: int, with_torch: bool = True) -> 
             unit: round(val, 2),
             "roofline": {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
                          "frac": round(ach / peak, 4), "traffic": load_traffic(name), "kernel": kernel,
-                         "kernel_ms": round(kern_ms, 5), **clock_normalised(ach, peak, bound, pwr)},
-            "power": pwr, **({"torch_same_device": ref} if ref else {})}
+                         "kernel_ms": round(kern_ms, 5)},
+            "power": None, **({"torch_same_device": ref} if ref else {}),
+            "power_job": lambda window_s: power_window(lambda i: fn(*args), kern_ms, window_s)}
 
 
 def cpu_description() -> str:
@@ -507,7 +518,7 @@ def torch_same_device(fn, args_fn, steps: int, warmup: int, flops: float, nbytes
     """The same op through torch on the same GPU (hipBLASLt / MIOpen), timed like ours
     -- the reference harness's comparison (tools/bench.py:67-104, speedup at :172).
     Context only: never part of the measured path."""
-    wall_ms, kern_ms, _ = timed_region(lambda i: fn(*args_fn(i)), steps, warmup, power_window_s=0.0)
+    wall_ms, kern_ms = timed_region(lambda i: fn(*args_fn(i)), steps, warmup)
     out = {"ms_per_step": round(wall_ms, 5), "kernel_ms": round(kern_ms, 5)}
     if hbm:
         out["GB/s"] = round(nbytes / (kern_ms * 1e-3) / 1e9, 1)
@@ -545,7 +556,7 @@ def roofline(r: dict, name: str) -> dict:
         ach, peak, unit, bound = r["kernel_tflops"], PEAK[c["dtype"]], "TFLOP/s", "mfma"
     return {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
             "frac": round(ach / peak, 4), "traffic": load_traffic(name), "kernel": r["kernel"],
-            "kernel_ms": round(r["kernel_ms"], 5), **clock_normalised(ach, peak, bound, r["power"])}
+            "kernel_ms": round(r["kernel_ms"], 5)}
 
 
 def main() -> int:
@@ -594,16 +605,16 @@ def main() -> int:
         return 0
     if args.caller:
         log(f"timing {args.caller} ({args.warmup} warm-up + {args.steps} steps)")
-        print(json.dumps({args.caller: time_caller(args.caller, args.steps, args.warmup)}), flush=True)
+        r = time_caller(args.caller, args.steps, args.warmup, not args.no_torch)
+        r.pop("power_job")
+        print(json.dumps({args.caller: r}), flush=True)
         return 0
     with_torch = not args.no_torch
-    set_power_window(args.power_window)
 
     def headline():
         log(f"timing {args.config} ({args.warmup} warm-up + {args.steps} steps)")
         r = time_gpu(args.config, args.steps, args.warmup, with_torch)
-        log(f"{args.config}: {r['ms_per_step']:.4f} ms/step, {r['tflops']:.1f} TFLOP/s, {r['gbs']:.0f} GB/s, "
-            f"power {r['power']}")
+        log(f"{args.config}: {r['ms_per_step']:.4f} ms/step, {r['tflops']:.1f} TFLOP/s, {r['gbs']:.0f} GB/s")
         return r
 
     head = headline() if args.headline_first or args.no_others else None
@@ -619,8 +630,9 @@ def main() -> int:
                                 "ms_per_step": round(r["ms_per_step"], 5),
                                 **({"GB/s": round(r["gbs"], 1)} if c.get("hbm") else
                                    {"TFLOP/s": round(r["tflops"], 2)}),
-                                "roofline": roofline(r, name), "power": r["power"],
-                                **({"torch_same_device": r["torch_same_device"]} if with_torch else {})}
+                                "roofline": roofline(r, name), "power": None,
+                                **({"torch_same_device": r["torch_same_device"]} if with_torch else {}),
+                                "power_job": r["power_job"]}
     callers = {}
     if not args.no_others and not args.no_callers:
         for name in CALLERS:
@@ -647,8 +659,18 @@ def main() -> int:
         "config": {"workload": f"{args.config}: {c['desc']}", "M": c["M"], "N": c["N"], "K": c["K"],
                    "accumulate": "fp32", "kernel": head["kernel"], "plan": head["plan"]},
         "roofline": roofline(head, args.config),
-        "power": head["power"],
+        "power": None,
     }
+    # power and clock of every workload, each over a window of back-to-back calls, now that
+    # all timed regions are done
+    jobs = [(line, head["power_job"])] + [(o, o.pop("power_job")) for o in others.values()] + \
+           [(cl, cl.pop("power_job")) for cl in callers.values()]
+    for obj, job in jobs:
+        obj["power"] = job(args.power_window)
+        obj["roofline"].update(clock_normalised(obj["roofline"]["achieved"], obj["roofline"]["peak"],
+                                                obj["roofline"]["bound"], obj["power"]))
+    del jobs, head["power_job"]
+    torch.cuda.empty_cache()
     if with_torch:
         line["torch_same_device"] = head["torch_same_device"]
     if not args.no_cpu:
