@@ -16,7 +16,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libc
 
 F16, BF16, F32 = 0, 1, 2
 B_KN, B_NK = 0, 1
-OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_TOO_LARGE, ERR_WORKSPACE = 0, -1, -2, -3, -4
+OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_TOO_LARGE, ERR_WORKSPACE, ERR_SCRATCH = 0, -1, -2, -3, -4, -5
+SCRATCH_BYTES = 64 << 20
 BIAS_PER_ROW = 1
 
 # Exported symbols and their C signatures, as declared in include/cmpext3_gemm.h.
@@ -38,6 +39,8 @@ SIGNATURES = {
     "cmpext3_gemm_call_workspace_size": (_i64, [_p]),
     "cmpext3_gemm_call_describe": (_i, [_p, _cp, _i]),
     "cmpext3_gemm_run": (_i, [_p, _p, _i64, _p]),
+    "cmpext3_gemm_ex_noalloc": (_i, [_i, _i, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p,
+                                     _i, _i, _i, _i, _p]),
     "cmpext3_status_string": (_cp, [_i]),
     "cmpext3_version": (_cp, []),
 }
@@ -140,6 +143,13 @@ def run(call: Call, workspace=None, workspace_bytes: int | None = None, stream=N
     if workspace_bytes is None:
         workspace_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     return lib().cmpext3_gemm_run(ctypes.byref(call), _ptr(workspace), workspace_bytes, _stream_handle(stream))
+
+
+def gemm_ex_noalloc(dtype: int, layout: int, A, lda: int, stride_a: int, B, ldb: int, stride_b: int, C,
+                    ldc: int, stride_c: int, bias, M: int, N: int, K: int, batch: int = 1, stream=None) -> int:
+    """Call cmpext3_gemm_ex_noalloc (the library's static scratch buffer as workspace)."""
+    return lib().cmpext3_gemm_ex_noalloc(dtype, layout, _ptr(A), lda, stride_a, _ptr(B), ldb, stride_b, _ptr(C),
+                                         ldc, stride_c, _ptr(bias), M, N, K, batch, _stream_handle(stream))
 
 
 def conv2d_1x1(dtype: int, inp, weight, bias, out, batch: int, c_in: int, c_out: int, hw: int,

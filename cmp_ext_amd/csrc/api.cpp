@@ -378,6 +378,9 @@ extern "C" const char* cmpext3_status_string(int status) {
     case CMPEXT3_ERR_WORKSPACE:
       return "workspace missing, not 16-byte aligned or smaller than the prepared call needs "
              "(cmpext3_gemm_call_workspace_size)";
+    case CMPEXT3_ERR_SCRATCH:
+      return "the call needs more workspace than the library's static scratch buffer holds "
+             "(CMPEXT3_SCRATCH_BYTES); use cmpext3_gemm_ex with a workspace";
     default:
       if (status > 0) return hipGetErrorString((hipError_t)status);
       return "unknown status";

@@ -33,6 +33,7 @@ extern "C" {
 #define CMPEXT3_ERR_UNSUPPORTED (-2)  /* unknown dtype / layout */
 #define CMPEXT3_ERR_TOO_LARGE (-3)    /* a size or stride does not fit the kernels' 32-bit offsets */
 #define CMPEXT3_ERR_WORKSPACE (-4)    /* a prepared call got less (or less aligned) workspace than it needs */
+#define CMPEXT3_ERR_SCRATCH (-5)      /* cmpext3_gemm_ex_noalloc: the call needs more than CMPEXT3_SCRATCH_BYTES */
 
 /* Element types. */
 #define CMPEXT3_F16 0
@@ -159,6 +160,32 @@ int cmpext3_gemm_prepare(cmpext3_gemm_call* call, int dtype, int b_layout,
 int64_t cmpext3_gemm_call_workspace_size(const cmpext3_gemm_call* call);
 int cmpext3_gemm_call_describe(const cmpext3_gemm_call* call, char* buf, int buflen);
 int cmpext3_gemm_run(const cmpext3_gemm_call* call, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * cmpext3_gemm_ex without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the call runs exactly the plan
+ * cmpext3_gemm_ex would run with all the workspace it asks for, with the
+ * library's own static device scratch buffer of CMPEXT3_SCRATCH_BYTES (64 MiB,
+ * held by every GPU the library runs on until the process ends) as that
+ * workspace.  It calls no allocating routine.  A call whose plan needs more
+ * than that (zero-padded copies of large unaligned operands, split-K partials
+ * of very large products) returns CMPEXT3_ERR_SCRATCH and launches nothing.
+ * The scratch contents need no clearing: every byte a call writes is read back
+ * by the same call.  All calls on one GPU share its buffer, so calls that may
+ * overlap on one GPU (other streams, other threads) race; order them on one
+ * stream.  The first call on a GPU must be made with that GPU current; it looks
+ * up the buffer's address there.
+ * No counterpart in the reference (its launchers take no workspace at all,
+ * src/main.cpp:12-14); it is for callers that cannot allocate.
+ */
+#define CMPEXT3_SCRATCH_BYTES (64ll << 20)
+int cmpext3_gemm_ex_noalloc(int dtype, int b_layout,
+                            const void* A, int64_t lda, int64_t stride_a,
+                            const void* B, int64_t ldb, int64_t stride_b,
+                            void* C, int64_t ldc, int64_t stride_c,
+                            const void* bias,
+                            int M, int N, int K, int batch, void* stream);
 
 /*
  * Bytes of workspace cmpext3_gemm_ex can use for these arguments (zero-padded
