@@ -26,6 +26,18 @@ int align_of(const void* ptr) {
   return a;
 }
 
+// The tile kernel for the element type and B layout, with whole-step loads when K
+// (and every split's K range) is a multiple of 64.
+hipError_t launch_tile(int dtype, KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s) {
+  const bool ragged = p.K % 64 != 0 || (p.splits > 1 && p.ksplit % 64 != 0);
+  if (dtype == kF16) {
+    if (lay == kKN) return ragged ? launch_tile_f16_kn_ragged(id, p, grid, s) : launch_tile_f16_kn_whole(id, p, grid, s);
+    return ragged ? launch_tile_f16_nk_ragged(id, p, grid, s) : launch_tile_f16_nk_whole(id, p, grid, s);
+  }
+  if (lay == kKN) return ragged ? launch_tile_bf16_kn_ragged(id, p, grid, s) : launch_tile_bf16_kn_whole(id, p, grid, s);
+  return ragged ? launch_tile_bf16_nk_ragged(id, p, grid, s) : launch_tile_bf16_nk_whole(id, p, grid, s);
+}
+
 hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p, dim3 grid, void* ws,
                     hipStream_t s) {
   const BLayout lay = (BLayout)layout;
@@ -45,14 +57,13 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
         q.ksplit = plan.ksplit;
         q.partials = (float*)ws;
         const dim3 g(grid.x, grid.y, grid.z * plan.splits);
-        hipError_t e = dtype == kF16 ? launch_tile_f16(plan.kernel, lay, q, g, s) : launch_tile_bf16(plan.kernel, lay, q, g, s);
+        hipError_t e = launch_tile(dtype, plan.kernel, lay, q, g, s);
         if (e == hipSuccess) e = launch_skinny_reduce((DType)dtype, p, (const float*)ws, plan.splits, (int)grid.z, s);
         return e;
       }
       [[fallthrough]];
     case kTile64x256:
-      return dtype == kF16 ? launch_tile_f16(plan.kernel, lay, p, grid, s)
-                           : launch_tile_bf16(plan.kernel, lay, p, grid, s);
+      return launch_tile(dtype, plan.kernel, lay, p, grid, s);
     case kSkinny:
       return launch_skinny((DType)dtype, plan.mb, p, grid, s);
     case kSkinnyNK:

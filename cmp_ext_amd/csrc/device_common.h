@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "gemm_params.h"
 
 namespace cmpext3 {
@@ -52,6 +54,20 @@ __device__ __forceinline__ void dma_load16(i32x4 rsrc, uint32_t voff, uint32_t l
                : "v"(voff), "s"(rsrc), "s"(lds_addr)
                : "memory", "m0");
 }
+// LDS DMA of 16 bytes per lane from global (rsrc + soff + voff) to LDS
+// (lds_base + DST + 16 * lane): M0 = lds_base + DST (the addition is left to
+// the compiler, which knows it sets SCC; then the one wait state an M0 write
+// needs before an LDS DMA reads it); soff is an SGPR byte offset that advances
+// along K without rebuilding the descriptor (it is part of the range check,
+// like voff).
+template <uint32_t DST>
+__device__ __forceinline__ void dma_load16_m0(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base,
+                                              std::integral_constant<uint32_t, DST> = {}) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %3 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(lds_base + DST), "s"(soff)
+               : "memory", "m0");
+}
 // Same with 4 bytes per lane (LDS destination lds_addr + 4 * lane): any
 // 4-byte-aligned source, e.g. fp32 rows of odd length.
 __device__ __forceinline__ void dma_load4(i32x4 rsrc, uint32_t voff, uint32_t lds_addr) {
@@ -74,6 +90,11 @@ __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t
 __device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
 }
+// Cache policy of buffer loads and stores that are coherent across the whole
+// device (the sc1 scope bit): a store reaches the memory side instead of staying
+// in the issuing XCD's L2, and a load does not hit a stale line there.
+constexpr int kCoherent = 16;
+
 // Vector store of 4 bytes; an offset past num_records (kBufOOB) is dropped by
 // the hardware, which is how edge elements are masked without branches.
 __device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {

@@ -8,8 +8,16 @@
 
 namespace cmpext3 {
 
-hipError_t launch_tile_f16(KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
-hipError_t launch_tile_bf16(KernelId id, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
+// f16/bf16 tile kernels, one entry per (type, B layout, K check): "whole" when K
+// (every split's range) is a multiple of 64, "ragged" otherwise.
+hipError_t launch_tile_f16_kn_whole(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_tile_f16_kn_ragged(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_tile_f16_nk_whole(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_tile_f16_nk_ragged(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_tile_bf16_kn_whole(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_tile_bf16_kn_ragged(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_tile_bf16_nk_whole(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_tile_bf16_nk_ragged(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s);
 hipError_t launch_skinny(DType dt, int mb, const GemmParams& p, dim3 grid, hipStream_t s);
 hipError_t launch_skinny_nk(DType dt, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s);
 hipError_t launch_skinny_wide(DType dt, int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid,

@@ -86,8 +86,10 @@ struct Tile16Shape {
   static constexpr int A_BYTES = BM * ROW;
   static constexpr int B_PITCH = KN ? (BN * 2 + 255) / 256 * 256 : ROW;  // bytes per LDS row of B
   static constexpr int B_BYTES = KN ? BK * B_PITCH : (BN + 63) / 64 * 64 * ROW;  // rows >= BN are OOB
-  static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int LDS = 2 * STAGE;
+  // LDS: the two ring slots of A, then the two of B, so that a fragment read of either
+  // slot is a fixed base register plus an immediate offset below 64 KiB
+  static constexpr int B_REGION = 2 * A_BYTES;
+  static constexpr int LDS = 2 * (A_BYTES + B_BYTES);
   static constexpr int A_DMA = A_BYTES / 1024 / NW;  // 1 KB LDS-DMA loads per wave per step
   static constexpr int B_DMA = B_BYTES / 1024 / NW;
   static constexpr int DMA = A_DMA + B_DMA;
@@ -95,6 +97,7 @@ struct Tile16Shape {
   static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "whole DMA loads per wave");
   static_assert(LDS <= 160 * 1024, "LDS budget");
   static_assert(DMA <= 63, "vmcnt range");
+  static_assert(A_BYTES + 14 * 2048 <= 65535 && B_BYTES + 36 * B_PITCH <= 65535, "immediate LDS offsets");
 };
 
 // BIAS: 0 none, 1 per column of C (Linear), 2 per row (conv 1x1).  A kernel per
@@ -102,7 +105,10 @@ struct Tile16Shape {
 // accumulators in AGPRs through the main loop.
 // SPLITK: grid.z = batch * p.splits; this workgroup sums its split's K range and
 // stores the fp32 sums (no bias, no rounding) into p.partials.
-template <typename T, bool KN, int BM, int BN, int WM, int WN, int BIAS, int MINB, bool SPLITK = false>
+// KCHECK: K (every split's K range) is not a multiple of 64, so the loads compare
+// each piece's k with K; otherwise they load whole steps unchecked.
+template <typename T, bool KN, int BM, int BN, int WM, int WN, int BIAS, int MINB, bool SPLITK = false,
+          bool KCHECK = false>
 __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const GemmParams p) {
   using S = Tile16Shape<BM, BN, KN, WM, WN>;
   constexpr int FM = S::FM, FN = S::FN;
@@ -154,18 +160,35 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
       b_kx[i] = 8 * chunk;
     }
   }
-  // LDS-DMA load d (A pieces first, then B) of K step kt into ring slot kt % 2;
-  // every k is checked against K, so steps at or past the end load zeros.
-  auto dma_piece = [&](int kt, int d) {
+  // LDS-DMA load d (A pieces first, then B) of K step kt into ring slot kt % 2.  A (and B
+  // as [N,K]) keep one descriptor at the tile base and advance along K through the SGPR
+  // offset; B as [K,N] gets a descriptor per step.  The destination goes through M0
+  // (one s_add per piece from a per-wave base).  With CHECK each piece's k is compared
+  // with K; a step at or past the end loads through an empty descriptor (num_records 0:
+  // the hardware writes zeros and reads no memory), so the loop needs no branch for it.
+  const i32x4 rsrc_a = make_rsrc_sgpr(Abase);
+  const i32x4 rsrc_b_nk = make_rsrc_sgpr(Bbase);
+  const uint32_t lds_a = lds_addr(smem) + (uint32_t)(wave * S::A_DMA * 1024);
+  const uint32_t lds_b = lds_addr(smem) + (uint32_t)(S::B_REGION + wave * S::B_DMA * 1024);
+  const int nk_all = (K + S::BK - 1) / S::BK;
+  auto dma_piece = [&](int kt, auto slotc, auto dc, auto checkc) {
+    constexpr int slot = decltype(slotc)::value, d = decltype(dc)::value;
+    constexpr bool check = decltype(checkc)::value;
     const int k0 = kt * S::BK;
-    const uint32_t sA = lds_addr(smem) + (uint32_t)((kt & 1) * S::STAGE);
-    const int krem = K - k0;
-    if (d < S::A_DMA) {
-      dma_load16(make_rsrc_sgpr(Abase + k0), a_kx[d] < krem ? a_off[d] : kBufOOB, sA + (wave * S::A_DMA + d) * 1024);
+    const bool live = kt < nk_all;  // wave-uniform
+    if constexpr (d < S::A_DMA) {
+      constexpr uint32_t dst = (uint32_t)(slot * S::A_BYTES + d * 1024);
+      const uint32_t voff = !check || a_kx[d] < K - k0 ? a_off[d] : kBufOOB;
+      i32x4 r = rsrc_a;
+      r[2] = live ? (int)kBufRecords : 0;
+      dma_load16_m0(r, voff, (uint32_t)k0 * (uint32_t)sizeof(T), lds_a, std::integral_constant<uint32_t, dst>{});
     } else {
-      const int i = d - S::A_DMA;
-      dma_load16(make_rsrc_sgpr(KN ? Bbase + (int64_t)k0 * ldb : Bbase + k0), b_kx[i] < krem ? b_off[i] : kBufOOB,
-                 sA + S::A_BYTES + (wave * S::B_DMA + i) * 1024);
+      constexpr int i = d - S::A_DMA;
+      constexpr uint32_t dst = (uint32_t)(slot * S::B_BYTES + i * 1024);
+      const uint32_t voff = !check || b_kx[i] < K - k0 ? b_off[i] : kBufOOB;
+      i32x4 r = KN ? make_rsrc_sgpr(Bbase + (int64_t)(live ? k0 : 0) * ldb) : rsrc_b_nk;
+      r[2] = live ? (int)kBufRecords : 0;
+      dma_load16_m0(r, voff, KN ? 0u : (uint32_t)k0 * (uint32_t)sizeof(T), lds_b, std::integral_constant<uint32_t, dst>{});
     }
   };
 
@@ -184,11 +207,13 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
 #pragma unroll
     for (int j = 0; j < (KN ? FN : 2); ++j) {
       const int cb = (wn * S::WTN + 16 * j + 4 * (r16 & 3)) * 2;  // byte column
-      fb_off[j] = kn_off(kr, S::B_PITCH, cb);  // + (32s + 4 half) rows keeps both swizzle terms
+      // + (32s + 4 half) rows keeps both swizzle terms; the B region's start is folded in so
+      // that the remaining offsets fit a read's immediate
+      fb_off[j] = S::B_REGION + kn_off(kr, S::B_PITCH, cb);
     }
   } else {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) fb_off[s] = lds_off128(wn * S::WTN + r16, 4 * s + G);
+    for (int s = 0; s < 2; ++s) fb_off[s] = S::B_REGION + lds_off128(wn * S::WTN + r16, 4 * s + G);
   }
 
   f32x4 acc[FM][FN];
@@ -202,14 +227,15 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
   // LDS read r of sub-step s of step kt into fragment buffer buf: r < FM reads A block r;
   // then B (two transposing reads per block for [K,N], one ds_read_b128 for [N,K]).
   constexpr int RD = FM + (KN ? 2 : 1) * FN;
-  auto read_one = [&](int kt, int s, int buf, auto rc) {
-    constexpr int r = decltype(rc)::value;
-    const unsigned char* st = smem + (kt & 1) * S::STAGE;
+  auto read_one = [&](auto slotc, int s, int buf, auto rc) {
+    constexpr int r = decltype(rc)::value, slot = decltype(slotc)::value;
+    const unsigned char* sa = smem + slot * S::A_BYTES;
+    const unsigned char* sb = smem + slot * S::B_BYTES;  // fb_off includes the B region's start
     if constexpr (r < FM) {
-      fa[buf][r] = *(const u32x4*)(st + fa_off[s] + r * 16 * S::ROW);
+      fa[buf][r] = *(const u32x4*)(sa + fa_off[s] + r * 16 * S::ROW);
     } else if constexpr (KN) {
       constexpr int j = (r - FM) >> 1, half = (r - FM) & 1;
-      const unsigned char* q = st + S::A_BYTES + fb_off[j] + (32 * s + 4 * half) * S::B_PITCH;
+      const unsigned char* q = sb + fb_off[j] + (32 * s + 4 * half) * S::B_PITCH;
       const u32x2 v = __builtin_bit_cast(
           u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q));
       if constexpr (half == 0) {
@@ -221,48 +247,59 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
       }
     } else {
       constexpr int j = r - FM;
-      fb[buf][j] = *(const u32x4*)(st + S::A_BYTES + fb_off[s] + j * 16 * S::ROW);
+      fb[buf][j] = *(const u32x4*)(sb + fb_off[s] + j * 16 * S::ROW);
     }
   };
-  // One 32-k sub-step of MFMAs on fragment buffer BUF; slot x also issues read
-  // r * X / RD == x of sub-step (rkt, rs) into the other buffer and, when WITH_DMA,
-  // DMA piece d * X / DMA == x of step dkt.
+  // One 32-k sub-step of MFMAs on fragment buffer BUF; MFMA slot x also issues read
+  // r * X / RD == x of sub-step RS of ring slot RSLOT into the other buffer and, for
+  // DMA mode 1 (full step) or 2 (the step holding K's end), DMA piece d * X / DMA == x of
+  // step dkt into ring slot DSLOT.
   constexpr int X = FM * FN;
-  auto substep = [&](auto bufc, int rkt, int rs, auto dmac, int dkt) {
+  auto substep = [&](auto bufc, auto rslotc, int rs, auto dmac, int dkt, auto dslotc) {
     constexpr int buf = decltype(bufc)::value;
-    constexpr bool with_dma = decltype(dmac)::value;
+    constexpr int dma = decltype(dmac)::value;
     static_for<X>([&](auto xc) {
       constexpr int x = decltype(xc)::value;
       constexpr int i = x / FN, j = x % FN;
       acc[i][j] = Mfma<T>::mma(fb[buf][j], fa[buf][i], acc[i][j]);
       static_for<RD>([&](auto rc) {
-        if constexpr (decltype(rc)::value * X / RD == x) read_one(rkt, rs, buf ^ 1, rc);
+        if constexpr (decltype(rc)::value * X / RD == x) read_one(rslotc, rs, buf ^ 1, rc);
       });
-      if constexpr (with_dma) {
+      if constexpr (dma != 0) {
         static_for<S::DMA>([&](auto dc) {
-          constexpr int d = decltype(dc)::value;
-          if constexpr (d * X / S::DMA == x) dma_piece(dkt, d);
+          if constexpr (decltype(dc)::value * X / S::DMA == x)
+            dma_piece(dkt, dslotc, dc, std::integral_constant<bool, dma == 2>{});
         });
       }
       __builtin_amdgcn_sched_barrier(0);  // keep the slots in this order
     });
   };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  // K step kt from ring slot SLOT: the second half's fragments are read during the
+  // first sub-step; one barrier certifies that every read of the slot is done and
+  // that step kt+1 (the other slot) has landed; the second sub-step reads step
+  // kt+1's first fragments and loads step kt+2 into this slot (DMA mode as above).
+  auto step = [&](int kt, auto slotc, auto dmac) {
+    using Other = std::integral_constant<int, 1 - decltype(slotc)::value>;
+    substep(B0{}, slotc, 1, B0{}, 0, slotc);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" : : : "memory");
+    substep(B1{}, Other{}, 0, dmac, kt + 2, slotc);
+  };
 
   const int nk = (K + S::BK - 1) / S::BK;
   if (nk > 0) {
-#pragma unroll
-    for (int d = 0; d < S::DMA; ++d) dma_piece(0, d);
-#pragma unroll
-    for (int d = 0; d < S::DMA; ++d) dma_piece(1, d);
+    using Mode = std::integral_constant<int, KCHECK ? 2 : 1>;  // checked or whole-step loads
+    using Check = std::integral_constant<bool, KCHECK>;
+    static_for<S::DMA>([&](auto dc) { dma_piece(0, B0{}, dc, Check{}); });
+    static_for<S::DMA>([&](auto dc) { dma_piece(1, B1{}, dc, Check{}); });  // zeros if nk == 1
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(S::DMA) : "memory");  // step 0 landed
-    static_for<RD>([&](auto rc) { read_one(0, 0, 0, rc); });
-    using B0 = std::integral_constant<int, 0>;
-    using B1 = std::integral_constant<int, 1>;
-    for (int kt = 0; kt < nk; ++kt) {
-      substep(B0{}, kt, 1, std::false_type{}, 0);
-      // every read of slot kt done and step kt+1 landed (this wave), then barrier
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" : : : "memory");
-      substep(B1{}, kt + 1, 0, std::true_type{}, kt + 2);
+    static_for<RD>([&](auto rc) { read_one(B0{}, 0, 0, rc); });
+    // pairs of steps, ring slots 0 and 1 (two copies of the step's code: the slot offsets
+    // are immediates)
+    for (int kt = 0; kt < nk; kt += 2) {
+      step(kt, B0{}, Mode{});
+      if (kt + 1 < nk) step(kt + 1, B1{}, Mode{});
     }
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // no LDS DMA may outlive the workgroup
   }
@@ -368,22 +405,22 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
 }
 
 // Launches gemm_tile16_kernel (WM x WN waves, MINB workgroups per CU) with the
-// bias mode the arguments ask for.
-template <typename T, bool KN, int BM, int BN, int WM, int WN, int MINB>
-void launch_tile16(const GemmParams& p, dim3 grid, hipStream_t s) {
+// bias mode and the K split the arguments ask for.
+template <typename T, bool KN, int BM, int BN, int WM, int WN, int MINB, bool KCHECK>
+void launch_tile16_k(const GemmParams& p, dim3 grid, hipStream_t s) {
   const dim3 block(64 * WM * WN);
   if constexpr (BM >= 128) {
     if (p.splits > 1) {  // fp32 partials; the bias comes with the reduction
-      hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 0, MINB, true>), grid, block, 0, s, p);
+      hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 0, MINB, true, KCHECK>), grid, block, 0, s, p);
       return;
     }
   }
   if (p.bias == nullptr)
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 0, MINB>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 0, MINB, false, KCHECK>), grid, block, 0, s, p);
   else if (p.bias_row)
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 2, MINB>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 2, MINB, false, KCHECK>), grid, block, 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 1, MINB>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 1, MINB, false, KCHECK>), grid, block, 0, s, p);
 }
 
 }  // namespace cmpext3

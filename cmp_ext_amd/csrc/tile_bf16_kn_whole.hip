@@ -1,0 +1,4 @@
+// bf16 tiles, B given as [K, N], K a multiple of 64 (whole-step loads).
+#include "tile_inst.h"
+
+CMPEXT3_TILE_TU(launch_tile_bf16_kn_whole, __bf16, true, false)

@@ -1,0 +1,4 @@
+// f16 tiles, B given as [K, N], K not a multiple of 64 (checked loads).
+#include "tile_inst.h"
+
+CMPEXT3_TILE_TU(launch_tile_f16_kn_ragged, _Float16, true, true)
