@@ -62,6 +62,7 @@ CONFIGS = {
                              desc="fp32_matmul 4097x2049 @ 2049x3001 (ragged)"),
 }
 HEADLINE = "cfg2_fp16_4096"
+ORDER = ["cfg4_fp16_skinny", "cfg5_fp32_ragged", "cfg3_bf16_mlp", "cfg2_fp16_4096"]
 
 # The reference callers at the reference benchmark's shapes (fp16, its first suite).
 CALLERS = {
@@ -574,6 +575,8 @@ def main() -> int:
     ap.add_argument("--headline-first", action="store_true",
                     help="time the headline workload before the other configs and callers (by default it is "
                          "timed last, once the GPU's clocks have left their idle state)")
+    ap.add_argument("--callers-first", action="store_true",
+                    help="time the linear / bmm / conv2d callers before the configurations")
     ap.add_argument("--power-window", type=float, default=POWER_WINDOW_S, metavar="S",
                     help="after each workload's timed steps, run it back to back for S seconds while reading "
                          "board power and shader clock (0: skip)")
@@ -619,8 +622,15 @@ def main() -> int:
 
     head = headline() if args.headline_first or args.no_others else None
     others = {}
-    if not args.no_others:
-        for name in CONFIGS:
+
+    def time_callers(out):
+        for name in CALLERS:
+            log(f"timing {name}")
+            out[name] = time_caller(name, args.steps, args.warmup, with_torch)
+            log(f"{name}: {out[name]['ms_per_step']:.4f} ms/step")
+
+    def time_others(names):
+        for name in names:
             if name != args.config:
                 log(f"timing {name}")
                 r = time_gpu(name, args.steps, args.warmup, with_torch)
@@ -633,12 +643,18 @@ def main() -> int:
                                 "roofline": roofline(r, name), "power": None,
                                 **({"torch_same_device": r["torch_same_device"]} if with_torch else {}),
                                 "power_job": r["power_job"]}
+    # Order: the short and unthrottled workloads first (skinny, fp32), then the callers,
+    # then the large 16-bit products, so that those are timed once the clocks have left
+    # their idle state (each workload still gets exactly its W warm-up calls)
     callers = {}
-    if not args.no_others and not args.no_callers:
-        for name in CALLERS:
-            log(f"timing {name}")
-            callers[name] = time_caller(name, args.steps, args.warmup, with_torch)
-            log(f"{name}: {callers[name]['ms_per_step']:.4f} ms/step")
+    if not args.no_others:
+        if not args.no_callers and args.callers_first:
+            time_callers(callers)
+        time_others([n for n in ORDER if n in ("cfg4_fp16_skinny", "cfg5_fp32_ragged")])
+        if not args.no_callers and not args.callers_first:
+            time_callers(callers)
+        time_others([n for n in ORDER if n not in ("cfg4_fp16_skinny", "cfg5_fp32_ragged")])
+        others = {n: others[n] for n in CONFIGS if n in others}
     if head is None:
         head = headline()
     c = CONFIGS[args.config]
