@@ -64,6 +64,8 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
       [[fallthrough]];
     case kTile64x256:
       return launch_tile(dtype, plan.kernel, lay, p, grid, s);
+    case kStream64x128:
+      return launch_stream((DType)dtype, p, grid, s);
     case kSkinny:
       return launch_skinny((DType)dtype, plan.mb, p, grid, s);
     case kSkinnyNK:
@@ -130,6 +132,7 @@ int prepare(Prepared* pc, int dtype, int b_layout, const void* A, int64_t lda, i
   r.align_c = align_of(C);
   r.align = std::min(std::min(r.align_a, r.align_b), r.align_c);
   r.has_bias = bias != nullptr;
+  r.bias_row = bias != nullptr && bias_row != 0;
   r.batch = batch;
   r.ws_bytes = std::max<int64_t>(0, workspace_limit);
   Plan plan;

@@ -40,6 +40,7 @@ struct Request {
                                   // address never restricts the kernel choice
   bool b_cols_padded;             // B ([K, N]) has zero columns up to a multiple of 8 (planner use)
   bool has_bias;
+  bool bias_row;  // the bias is one value per row of C (a 1x1 convolution's), not per column
   int64_t batch;
   int64_t ws_bytes;  // workspace the caller provides (0: none)
 };

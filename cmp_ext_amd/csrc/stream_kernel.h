@@ -1,0 +1,225 @@
+// Short-K f16/bf16 GEMM over many columns: C[b] = A * B[b] (+ bias per row),
+// M <= 64, K <= 128, B as [K,N] -- the shape of a 1x1 convolution over NCHW
+// activations (A = the weight, shared by every batch entry; B[b] = one image's
+// [C_in][H*W]; C[b] = its [C_out][H*W]); counterpart of the reference's conv2d
+// routed through its GEMM (csrc/main.cpp:402-424).
+//
+// Such a product moves ~3 bytes per 64 flops: it is bound by streaming B in and
+// C out, and a tile kernel that holds one 64 x 256 tile per workgroup leaves
+// each CU idle between its tiles' loads (measured 3.9 TB/s).  Here a persistent
+// workgroup per CU walks the 128-column tiles t = blockIdx.x, + gridDim.x, ...
+// (batch entry t / tiles_n) with
+//   * A held in registers for the whole kernel (64 x 128 as MFMA fragments);
+//   * B tiles ([K][128] = 32 KiB, rows of 256 bytes) streamed global -> LDS by
+//     LDS-DMA through a ring of four slots, three tiles in flight;
+//   * per tile 8 MFMAs of 16x16x32 per wave and K/32 sub-steps (4 waves, each
+//     all 64 rows x 32 columns), B fragments by ds_read_b64_tr_b16 as in the
+//     tile kernel's [K,N] path;
+//   * the tile's results staged in LDS (row-major, 16-byte chunks XOR-swizzled by
+//     row) and written during the next tile, after its barrier: each wave stores
+//     16 whole rows of 256 bytes with non-temporal 16-byte stores (full cache
+//     lines that go straight to HBM instead of waiting in L2 as dirty lines;
+//     measured on MI355X for the 64 x 16384 x 128 x 64 convolution: 62.4 us
+//     against 84.5 us for the MFMA layout's 64-byte row pieces through L2, and
+//     72.3 us for those pieces non-temporal), out-of-range lanes masked by the
+//     descriptor, so that every iteration issues the same number of
+//     vector-memory instructions and one "s_waitcnt vmcnt" constant certifies
+//     the tile about to be read.
+// Requirements (checked by the selector): K <= 128 and K, N, lda, ldb, ldc
+// multiples of 8; A, B and C 16-byte aligned; one A for the whole batch
+// (batch 1 or stride_a 0); 64 * ldc * 2 and 128 * ldb * 2 below 2^31.
+#pragma once
+
+#include <type_traits>
+
+#include "device_common.h"
+#include "tile16_kernel.h"
+
+namespace cmpext3 {
+
+constexpr int kStreamN = 128;     // columns per tile
+constexpr int kStreamK = 128;     // largest K (rows of a ring slot)
+constexpr int kStreamSlots = 4;   // ring depth: three tiles in flight while one is read
+// Cache policy of the result stores: non-temporal (the nt bit of the buffer instruction).
+constexpr int kStreamStorePolicy = 2;
+
+// BIAS: 0 none, 2 one value per row of C (the convolution's per-channel bias).
+template <typename T, int BIAS>
+__global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p, int total_tiles) {
+  constexpr int PITCH = kStreamN * 2;            // bytes per k row of a slot
+  constexpr int SLOT = kStreamK * PITCH;         // 32 KiB
+  constexpr int P = SLOT / 1024 / 4;             // 1 KiB LDS-DMA loads per wave per tile
+  constexpr int FM = 4, FN = 2, KS = kStreamK / 32;
+  constexpr int Q = FM;                          // 16-byte stores per wave per tile
+  static_assert(2 * P + 2 * Q <= 63, "vmcnt range");
+  constexpr int STG = 64 * 256;                  // one tile's results, two buffers
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kStreamSlots * SLOT + 2 * STG];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, G = lane >> 4;
+  const int M = p.M, N = p.N, K = p.K;
+  const int tiles_n = p.tiles_n;
+  const int me = blockIdx.x, step = gridDim.x;
+  const int ntiles = total_tiles > me ? (total_tiles - me + step - 1) / step : 0;
+
+  // ---- A fragments (rows 16i + r16, k = 32s + 8G .. +7), zero past M and K ----
+  u32x4 fa[FM][KS];
+  {
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A);
+    static_for<FM * KS>([&](auto xc) {
+      constexpr int x = decltype(xc)::value, i = x / KS, s = x % KS;
+      const int m = 16 * i + r16, k = 32 * s + 8 * G;
+      fa[i][s] = buf_load16(ra, (m < M && k < K) ? (uint32_t)(m * p.lda + k) * 2u : kBufOOB);
+    });
+  }
+  float bias_m[FM] = {};
+  if constexpr (BIAS == 2) {
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.bias), 0, 2 * M, kBufWord3);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) bias_m[i] = from_bits<T>(buf_load2(rb, (uint32_t)(2 * (16 * i + r16))));
+  }
+  // Make these values definitions of an asm statement placed after a full wait: the
+  // compiler counts only its own vector-memory instructions, so a wait it derived for
+  // them inside the loop would also stall on the ring's loads.
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+#pragma unroll
+  for (int x = 0; x < FM * KS; ++x) asm volatile("" : "+v"(fa[x / KS][x % KS]));
+#pragma unroll
+  for (int i = 0; i < FM; ++i) asm volatile("" : "+v"(bias_m[i]));
+
+  // ---- DMA: piece q of wave w fills bytes (w*P + q) KiB of a slot = k rows 4(wP+q) .. +3 ----
+  uint32_t b_off[P];
+  int b_n[P];
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    int k, n;
+    dma_kn_geom(wave * P + q, lane, PITCH, k, n);
+    b_off[q] = k < K ? (uint32_t)(k * p.ldb + n) * 2u : kBufOOB;
+    b_n[q] = n;
+  }
+  const uint32_t lds_w = lds_addr(smem) + (uint32_t)(wave * P * 1024);
+  // Tile i of this workgroup into ring slot i % 4; tiles past the end load through an
+  // empty descriptor (no memory read, zeros into LDS) so every iteration issues P loads.
+  auto issue = [&](int i) {
+    const bool live = i < ntiles;
+    const int t = live ? me + i * step : 0;
+    const int bz = t / tiles_n, n0 = (t - bz * tiles_n) * kStreamN;
+    i32x4 r = make_rsrc_sgpr((const T*)p.B + (int64_t)bz * p.stride_b + n0);
+    r[2] = live ? (int)kBufRecords : 0;
+    const uint32_t base = lds_w + (uint32_t)((i % kStreamSlots) * SLOT);
+    static_for<P>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      const uint32_t voff = n0 + b_n[q] < N ? b_off[q] : kBufOOB;
+      dma_load16_m0(r, voff, 0u, base, std::integral_constant<uint32_t, (uint32_t)(q * 1024)>{});
+    });
+  };
+
+  // ---- fragment addresses ([k][n] slot, transposing reads as in the tile kernel) ----
+  uint32_t fb_off[FN];
+  const int kr = 8 * G + (r16 >> 2);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) fb_off[j] = kn_off(kr, PITCH, (32 * wave + 16 * j + 4 * (r16 & 3)) * 2);
+
+  // ---- results: after one permlane16 swap per dword, lane (r16, G) holds row 16i + r16,
+  // columns col .. col+7 of the tile; they go to staging buffer i % 2 as 16-byte chunk
+  // col/8 of the row, at chunk position (col/8) ^ (row % 16) (conflict-free writes and
+  // row reads) ----
+  const int col = 32 * wave + 16 * (G & 1) + 8 * (G >> 1);
+  unsigned char* const stg0 = smem + kStreamSlots * SLOT;
+  // The 4 x 256-byte-row stores of tile i by this wave (rows 16 wave .. +15, an empty
+  // descriptor when there is no tile i): always Q instructions.
+  auto store = [&](int i) {
+    const bool live = i >= 0 && i < ntiles;
+    const int t = live ? me + i * step : 0;
+    const int bz = t / tiles_n, n0 = (t - bz * tiles_n) * kStreamN;
+    T* cb = (T*)p.C + (int64_t)bz * p.stride_c + n0;
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(cb, 0, live ? (int)kBufRecords : 0, kBufWord3);
+    const unsigned char* stg = stg0 + (i & 1) * STG;
+    const int ch = lane & 15;
+    const bool col_ok = n0 + 8 * ch < N;
+    u32x4 v[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int row = 16 * wave + 4 * q + (lane >> 4);
+      v[q] = *(const u32x4*)(stg + row * 256 + ((ch ^ (row & 15)) << 4));
+    }
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int row = 16 * wave + 4 * q + (lane >> 4);
+      const uint32_t off = (col_ok && row < M) ? (uint32_t)(row * p.ldc + 8 * ch) * 2u : kBufOOB;
+      __builtin_amdgcn_raw_buffer_store_b128(v[q], rc, off, 0, kStreamStorePolicy);
+    }
+  };
+
+  static_for<kStreamSlots - 1>([&](auto ic) { issue(decltype(ic)::value); });
+  for (int i = 0; i < ntiles; ++i) {
+    // Tile i landed: after its loads (issued in iteration i-3) this wave issued the
+    // stores and loads of two more iterations (2P + 2Q instructions; 2P + Q and 2P
+    // for i = 1, 0), and vector-memory instructions complete in issue order.
+    if (i >= 2)
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(2 * P + 2 * Q) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(2 * P) : "memory");
+    // every wave is past tile i-1's reads (its slot takes tile i+3) and has staged
+    // tile i-1's results
+    store(i - 1);
+    issue(i + kStreamSlots - 1);
+
+    const unsigned char* sb = smem + (i % kStreamSlots) * SLOT;
+    u32x4 fb[KS][FN];
+    static_for<KS * FN * 2>([&](auto rc) {
+      constexpr int r = decltype(rc)::value, s = r / (2 * FN), j = (r / 2) % FN, half = r % 2;
+      typedef short s16x4 __attribute__((ext_vector_type(4)));
+      const unsigned char* q = sb + fb_off[j] + (32 * s + 4 * half) * PITCH;
+      const u32x2 v = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q));
+      if constexpr (half == 0) {
+        fb[s][j].x = v.x;
+        fb[s][j].y = v.y;
+      } else {
+        fb[s][j].z = v.x;
+        fb[s][j].w = v.y;
+      }
+    });
+    f32x4 acc[FM][FN];
+    static_for<FM * FN>([&](auto xc) {
+      constexpr int x = decltype(xc)::value;
+      acc[x / FN][x % FN] = f32x4{0.f, 0.f, 0.f, 0.f};
+    });
+    static_for<KS * FM * FN>([&](auto xc) {
+      constexpr int x = decltype(xc)::value, s = x / (FM * FN), i = (x / FN) % FM, j = x % FN;
+      acc[i][j] = Mfma<T>::mma(fb[s][j], fa[i][s], acc[i][j]);
+    });
+    // results -> staging buffer i % 2, last read by the stores of tile i-2 (iteration
+    // i-1), which every wave finished before this iteration's barrier
+    unsigned char* stg = stg0 + (i & 1) * STG;
+#pragma unroll
+    for (int ii = 0; ii < FM; ++ii) {
+      f32x4 v0 = acc[ii][0], v1 = acc[ii][1];
+      if constexpr (BIAS == 2) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v0[e] += bias_m[ii];
+          v1[e] += bias_m[ii];
+        }
+      }
+      uint32_t P0[2] = {pack2<T>(v0[0], v0[1]), pack2<T>(v0[2], v0[3])};
+      uint32_t P1[2] = {pack2<T>(v1[0], v1[1]), pack2<T>(v1[2], v1[3])};
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        const auto sw = __builtin_amdgcn_permlane16_swap(P0[w], P1[w], false, false);
+        P0[w] = sw[0];
+        P1[w] = sw[1];
+      }
+      const int row = 16 * ii + r16;
+      *(u32x4*)(stg + row * 256 + (((col >> 3) ^ (row & 15)) << 4)) = u32x4{P0[0], P0[1], P1[0], P1[1]};
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");  // the last tile is staged
+  store(ntiles - 1);
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // no LDS DMA may outlive the workgroup
+}
+
+}  // namespace cmpext3

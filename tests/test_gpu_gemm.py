@@ -25,7 +25,7 @@ CODE = {"fp16": cabi.F16, "bf16": cabi.BF16, "fp32": cabi.F32}
 MATMUL = {"fp16": cmpext3.fp16_matmul, "bf16": cmpext3.bf16_matmul, "fp32": cmpext3.fp32_matmul}
 KERNEL_NAMES = ["tile256x256", "tile256x224", "tile128x128", "tile64x256", "skinny", "skinny_wide", "skinny_nk",
                 "f32tile128x128",
-                "f32tile64x64", "f32tile96x64", "f32tile64x64k4", "f32tile16x64k4", "generic64x64"]
+                "f32tile64x64", "f32tile96x64", "f32tile64x64k4", "f32tile16x64k4", "generic64x64", "stream64x128"]
 SEEN_KERNELS = set()
 
 
@@ -729,6 +729,51 @@ def test_tiled_split_k_batched(dtype):
     _, desc1 = launched()
     if desc1.split()[0] == desc.split()[0] and desc1.split("splits=")[1].split()[0] == desc.split("splits=")[1].split()[0]:
         assert torch.equal(single[0], out[1])
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("M,N,K,batch,bias", [
+    (64, 8200, 128, 64, False),   # 65 column tiles per entry, the last one 8 columns wide
+    (40, 16384, 72, 32, True),    # ragged M and K, bias per row (4096 tiles: 16 per CU)
+    (1, 524288, 8, 1, False),     # one row, K = 8, one product of 4096 tiles
+])
+def test_stream_kernel(dtype, M, N, K, batch, bias):
+    """Short-K products over many columns with one A for the whole batch (the 1x1
+    convolution shape) through the C ABI: the streaming kernel, against the float64
+    oracle on sampled batch entries and an fp32 GPU product on all, deterministic."""
+    g = torch.Generator().manual_seed(M + K + batch)
+    a = (torch.randn(M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    b = torch.randn(batch, K, N, generator=g).to(DT[dtype])
+    bvec = torch.randn(M, generator=g).to(DT[dtype]) if bias else None
+    ag, bg = a.cuda(), b.cuda()
+    bvg = bvec.cuda() if bias else None
+    c = torch.full((batch, M, N), float("nan"), dtype=DT[dtype], device="cuda")
+    print(f"stream {dtype} M={M} N={N} K={K} batch={batch} bias={bias}", flush=True)
+    st, call = cabi.prepare(CODE[dtype], cabi.B_KN, ag, K, 0, bg, N, K * N, c, N, M * N, bvg, M, N, K, batch,
+                            cabi.BIAS_PER_ROW if bias else 0, 0)
+    assert st == cabi.OK
+    _, desc = cabi.describe(call)
+    SEEN_KERNELS.add(kernel_of(desc))
+    assert kernel_of(desc) == "stream64x128", desc
+    assert cabi.run(call) == cabi.OK
+    torch.cuda.synchronize()
+    assert not torch.isnan(c).any()
+    ref = torch.matmul(ag.float(), bg.float())
+    if bias:
+        ref = ref + bvg.float()[:, None]
+    e2 = ((c.double() - ref.double()).norm() / ref.double().norm()).item()
+    assert e2 <= O.TOLERANCE[dtype]
+    for i in sorted({0, batch // 2, batch - 1}):
+        r = O.matmul_f64(O.to_f64(a), O.to_f64(b[i]))
+        if bias:
+            r = r + O.to_f64(bvec)[:, None]
+        assert O.rel_frobenius(O.to_f64(c[i].cpu()), r) <= O.TOLERANCE[dtype], i
+    c2 = torch.empty_like(c)
+    st, call2 = cabi.prepare(CODE[dtype], cabi.B_KN, ag, K, 0, bg, N, K * N, c2, N, M * N, bvg, M, N, K, batch,
+                             cabi.BIAS_PER_ROW if bias else 0, 0)
+    assert st == cabi.OK and cabi.run(call2) == cabi.OK
+    torch.cuda.synchronize()
+    assert torch.equal(c, c2)
 
 
 def test_every_kernel_family_was_exercised():

@@ -4,7 +4,7 @@ import pytest
 from cmp_ext_amd import cabi
 
 K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKINNY_WIDE, K_F32_96, K_TILE64, \
-    K_SKINNY_NK, K_F32_64K4 = range(12)
+    K_SKINNY_NK, K_F32_64K4, K_F32_16K4, K_STREAM = range(14)
 
 
 @pytest.mark.parametrize("dtype,M,N,K,expect", [
@@ -42,11 +42,47 @@ def test_skinny_wide_needs_workspace():
 
 
 def test_skinny_m_batches_with_many_tiles_go_tiled():
-    # a 1x1 convolution over 64 images of 128x128 pixels: C_out = 64 rows, 128 column tiles each
+    # a product of 64 rows with 64 x 128 column tiles of 128: tiled (cabi.plan gives the
+    # batch entries their own A, so the streaming kernel, which shares one A, is out)
     kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 64, 16384, 128, batch=64)
     assert kid == K_TILE64, desc
     kid, desc = cabi.plan(cabi.F16, cabi.B_KN, 64, 16384, 128, batch=1)
     assert kid in (K_SKINNY, K_SKINNY_WIDE), desc       # 128 tiles alone would leave CUs idle
+
+
+def _prepared_kernel(dtype, M, N, K, batch, stride_a, flags=0, bias=None, lda=None, ldc=None, align=0,
+                     workspace_limit=0):
+    """Kernel id and description the C ABI plans for these pointers and pitches (no GPU:
+    prepare only; by default without a workspace)."""
+    lda = lda or K
+    ldc = ldc or N
+    a, b, c = 0x100000 + align, 0x40000000, 0x80000000
+    st, call = cabi.prepare(dtype, cabi.B_KN, a, lda, stride_a, b, N, K * N, c, ldc, M * ldc, bias, M, N, K,
+                            batch, flags, workspace_limit)
+    assert st == cabi.OK
+    return cabi.describe(call)
+
+
+def test_stream_kernel_for_convolution_shapes():
+    # a 1x1 convolution over 64 images of 128x128 pixels (the weight shared: stride_a 0,
+    # bias per output channel): 8192 column tiles of 128, 32 per CU
+    kid, desc = _prepared_kernel(cabi.F16, 64, 16384, 128, 64, 0, cabi.BIAS_PER_ROW, bias=0x1000)
+    assert kid == K_STREAM and "tile=64x128" in desc, desc
+    assert _prepared_kernel(cabi.BF16, 40, 16384, 72, 32, 0)[0] == K_STREAM      # 4096 tiles, ragged M, K
+    assert _prepared_kernel(cabi.F16, 1, 524288, 8, 1, 0)[0] == K_STREAM
+    assert _prepared_kernel(cabi.F16, 64, 8200, 128, 64, 0)[0] == K_STREAM       # 65 tiles per image
+    # not the streaming kernel: too few tiles per CU, K above 128, M above 64, one A per
+    # batch entry, a bias per column, a misaligned A, or rows of C not 16-byte multiples
+    assert _prepared_kernel(cabi.F16, 64, 16384, 128, 31, 0)[0] != K_STREAM
+    assert _prepared_kernel(cabi.F16, 64, 16384, 136, 64, 0)[0] != K_STREAM
+    assert _prepared_kernel(cabi.F16, 65, 16384, 128, 64, 0)[0] != K_STREAM
+    assert _prepared_kernel(cabi.F16, 64, 16384, 128, 64, 64 * 128)[0] != K_STREAM
+    assert _prepared_kernel(cabi.F16, 64, 16384, 128, 64, 0, 0, bias=0x1000)[0] != K_STREAM
+    assert _prepared_kernel(cabi.F16, 64, 16384, 128, 64, 0, align=8)[0] != K_STREAM
+    kid, desc = _prepared_kernel(cabi.F16, 64, 16384, 128, 64, 0, align=8, workspace_limit=1 << 20)
+    assert kid == K_STREAM and "padded=A" in desc, desc   # with a workspace: one aligned copy of A
+    assert _prepared_kernel(cabi.F16, 64, 16380, 128, 64, 0, ldc=16380)[0] != K_STREAM
+    assert _prepared_kernel(cabi.F32, 64, 16384, 128, 64, 0)[0] != K_STREAM
 
 
 def test_skinny_linear_weight_layout():
