@@ -62,7 +62,16 @@ CONFIGS = {
                              desc="fp32_matmul 4097x2049 @ 2049x3001 (ragged)"),
 }
 HEADLINE = "cfg2_fp16_4096"
-ORDER = ["cfg4_fp16_skinny", "cfg5_fp32_ragged", "cfg3_bf16_mlp", "cfg2_fp16_4096"]
+# Order in which the workloads are timed (the headline, wherever it appears, last unless
+# --headline-first).  A matrix-core-bound workload runs slower for its first ~20 ms of
+# calls while the shader clock settles under the power limit (MI355X, bf16 4096 x 14336 x
+# 4096 after 0.2 s idle: medians of successive groups of 20 calls 416, 377, 352, 342, then
+# 340 us; 358 us for the first group right after 40 ms of fp16 4096^3 calls), so with few
+# warm-up calls its timed steps include part of that ramp.  The order does not change this
+# (measured: timing the matrix-core-bound workloads right after each other moved no figure
+# by more than the run-to-run spread).
+ORDER = ["cfg4_fp16_skinny", "cfg5_fp32_ragged", "linear_fp16_4096", "bmm_fp16_16x1024",
+         "conv1x1_fp16_64x128x128x128", "cfg3_bf16_mlp", "cfg2_fp16_4096"]
 
 # The reference callers at the reference benchmark's shapes (fp16, its first suite).
 CALLERS = {
@@ -575,8 +584,8 @@ def main() -> int:
     ap.add_argument("--headline-first", action="store_true",
                     help="time the headline workload before the other configs and callers (by default it is "
                          "timed last, once the GPU's clocks have left their idle state)")
-    ap.add_argument("--callers-first", action="store_true",
-                    help="time the linear / bmm / conv2d callers before the configurations")
+    ap.add_argument("--order", default=",".join(ORDER),
+                    help="comma-separated order in which the configs and callers are timed")
     ap.add_argument("--power-window", type=float, default=POWER_WINDOW_S, metavar="S",
                     help="after each workload's timed steps, run it back to back for S seconds while reading "
                          "board power and shader clock (0: skip)")
@@ -623,38 +632,36 @@ def main() -> int:
     head = headline() if args.headline_first or args.no_others else None
     others = {}
 
-    def time_callers(out):
-        for name in CALLERS:
+    def time_one(name):
+        if name in CALLERS:
             log(f"timing {name}")
-            out[name] = time_caller(name, args.steps, args.warmup, with_torch)
-            log(f"{name}: {out[name]['ms_per_step']:.4f} ms/step")
+            callers[name] = time_caller(name, args.steps, args.warmup, with_torch)
+            log(f"{name}: {callers[name]['ms_per_step']:.4f} ms/step")
+            return
+        log(f"timing {name}")
+        r = time_gpu(name, args.steps, args.warmup, with_torch)
+        log(f"{name}: {r['ms_per_step']:.4f} ms/step, {r['tflops']:.1f} TFLOP/s, {r['gbs']:.0f} GB/s")
+        c = CONFIGS[name]
+        others[name] = {"desc": r["desc"], "kernel": r["kernel"], "plan": r["plan"],
+                        "ms_per_step": round(r["ms_per_step"], 5),
+                        **({"GB/s": round(r["gbs"], 1)} if c.get("hbm") else
+                           {"TFLOP/s": round(r["tflops"], 2)}),
+                        "roofline": roofline(r, name), "power": None,
+                        **({"torch_same_device": r["torch_same_device"]} if with_torch else {}),
+                        "power_job": r["power_job"]}
 
-    def time_others(names):
-        for name in names:
-            if name != args.config:
-                log(f"timing {name}")
-                r = time_gpu(name, args.steps, args.warmup, with_torch)
-                log(f"{name}: {r['ms_per_step']:.4f} ms/step, {r['tflops']:.1f} TFLOP/s, {r['gbs']:.0f} GB/s")
-                c = CONFIGS[name]
-                others[name] = {"desc": r["desc"], "kernel": r["kernel"], "plan": r["plan"],
-                                "ms_per_step": round(r["ms_per_step"], 5),
-                                **({"GB/s": round(r["gbs"], 1)} if c.get("hbm") else
-                                   {"TFLOP/s": round(r["tflops"], 2)}),
-                                "roofline": roofline(r, name), "power": None,
-                                **({"torch_same_device": r["torch_same_device"]} if with_torch else {}),
-                                "power_job": r["power_job"]}
-    # Order: the short and unthrottled workloads first (skinny, fp32), then the callers,
-    # then the large 16-bit products, so that those are timed once the clocks have left
-    # their idle state (each workload still gets exactly its W warm-up calls)
     callers = {}
     if not args.no_others:
-        if not args.no_callers and args.callers_first:
-            time_callers(callers)
-        time_others([n for n in ORDER if n in ("cfg4_fp16_skinny", "cfg5_fp32_ragged")])
-        if not args.no_callers and not args.callers_first:
-            time_callers(callers)
-        time_others([n for n in ORDER if n not in ("cfg4_fp16_skinny", "cfg5_fp32_ragged")])
+        order = [n for n in args.order.split(",") if n]
+        unknown = [n for n in order if n not in CONFIGS and n not in CALLERS]
+        if unknown:
+            raise SystemExit(f"bench.py: unknown workloads in --order: {unknown}")
+        for name in order:
+            if name == args.config or (name in CALLERS and args.no_callers):
+                continue
+            time_one(name)
         others = {n: others[n] for n in CONFIGS if n in others}
+        callers = {n: callers[n] for n in CALLERS if n in callers}
     if head is None:
         head = headline()
     c = CONFIGS[args.config]
