@@ -224,7 +224,7 @@ int make_plan_core(const Request& r, Plan* plan) {
     } else if (fast && r.layout == kKN && r.M <= 64 && r.K <= 128 && r.N % 8 == 0 && r.ldc % 8 == 0 &&
                (!batched || (r.stride_a == 0 && r.stride_c % 8 == 0)) && (!r.has_bias || r.bias_row) &&
                128 * r.ldb * 2 <= kIntMax && 64 * r.ldc * 2 <= kIntMax &&
-               cdiv(r.N, 128) * r.batch >= 16 * kNumCUs) {
+               cdiv(r.N, 128) * r.batch >= 16 * kNumCUs && cdiv(r.N, 128) * r.batch <= kIntMax) {
       // Short K over many columns with one A (a 1x1 convolution: weight x every image's
       // pixels): bound by streaming B in and C out, which persistent workgroups with
       // three tiles in flight do faster than one tile per workgroup once each has >= 16

@@ -83,6 +83,8 @@ def test_stream_kernel_for_convolution_shapes():
     assert kid == K_STREAM and "padded=A" in desc, desc   # with a workspace: one aligned copy of A
     assert _prepared_kernel(cabi.F16, 64, 16380, 128, 64, 0, ldc=16380)[0] != K_STREAM
     assert _prepared_kernel(cabi.F32, 64, 16384, 128, 64, 0)[0] != K_STREAM
+    assert _prepared_kernel(cabi.F16, 64, 4194296, 128, 256, 0)[0] == K_STREAM
+    assert _prepared_kernel(cabi.F16, 64, 4194296, 128, 70000, 0)[0] != K_STREAM   # > 2^31 tiles
 
 
 def test_skinny_linear_weight_layout():
