@@ -24,18 +24,37 @@ hipError_t launch(int mb, const GemmParams& p, dim3 grid, hipStream_t s) {
 }
 }  // namespace
 
-template <typename T, int SW>
+namespace {
+// The streamed operand (B, or W) of one launch is read with the non-temporal policy when it
+// is at least kStreamOnceBytes: a smaller one may still sit in the 256 MB Infinity Cache at
+// the next call, which the policy would give up (MI355X, fp16, operands rotating over four
+// buffers: 16 x 8192 x 8192 27.6 -> 26.1 us, W of 8192 x 8192 for one row 28.3 -> 25.0 us,
+// 14336 x 4096 for 16 rows 25.9 -> 23.3 us; 4096 x 4096, whose four copies fit the cache,
+// 7.9 -> 8.8 us).
+constexpr int64_t kStreamOnceBytes = 64ll << 20;
+bool stream_once(int64_t rows, int64_t cols, int64_t stride, unsigned batch) {
+  return rows * cols * 2 * (stride != 0 ? (int64_t)batch : 1) >= kStreamOnceBytes;
+}
+
+template <typename T, int SW, bool NT>
 hipError_t launch_nk(int mb, const GemmParams& p, dim3 grid, hipStream_t s) {
   const dim3 block(256);
   switch (mb) {  // 1 KB of each W row per stage for one 16-row block of A, 512 bytes otherwise
-    case 1: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 1, SW, 512>), grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 2, SW, 256>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 3, SW, 256>), grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, SW, 256>), grid, block, 0, s, p); break;
+    case 1: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 1, SW, 512, NT>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 2, SW, 256, NT>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 3, SW, 256, NT>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, SW, 256, NT>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
+template <typename T>
+hipError_t launch_nk(int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {
+  const bool nt = stream_once(p.N, p.K, p.stride_b, grid.z);
+  if (strip == 16) return nt ? launch_nk<T, 16, true>(mb, p, grid, s) : launch_nk<T, 16, false>(mb, p, grid, s);
+  return nt ? launch_nk<T, 32, true>(mb, p, grid, s) : launch_nk<T, 32, false>(mb, p, grid, s);
+}
+}  // namespace
 
 hipError_t launch_skinny(DType dt, int mb, const GemmParams& p, dim3 grid, hipStream_t s) {
   if (dt == kF16) return launch<_Float16>(mb, p, grid, s);
@@ -44,17 +63,22 @@ hipError_t launch_skinny(DType dt, int mb, const GemmParams& p, dim3 grid, hipSt
 }
 
 namespace {
-template <typename T>
+template <typename T, bool NT>
 hipError_t launch_wide(int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid, hipStream_t s) {
   const dim3 block(256);
   switch (mb) {
-    case 1: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 1>), grid, block, 0, s, p, ws, splits, ksplit); break;
-    case 2: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 2>), grid, block, 0, s, p, ws, splits, ksplit); break;
-    case 3: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 3>), grid, block, 0, s, p, ws, splits, ksplit); break;
-    case 4: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 4>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    case 1: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 1, NT>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    case 2: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 2, NT>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    case 3: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 3, NT>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    case 4: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 4, NT>), grid, block, 0, s, p, ws, splits, ksplit); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+template <typename T>
+hipError_t launch_wide(int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid, hipStream_t s) {
+  return stream_once(p.K, p.N, p.stride_b, grid.z) ? launch_wide<T, true>(mb, p, ws, splits, ksplit, grid, s)
+                                                   : launch_wide<T, false>(mb, p, ws, splits, ksplit, grid, s);
 }
 }  // namespace
 
@@ -106,8 +130,8 @@ hipError_t launch_skinny_reduce(DType dt, const GemmParams& p, const float* ws, 
   return hipGetLastError();
 }
 hipError_t launch_skinny_nk(DType dt, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {
-  if (dt == kF16) return strip == 16 ? launch_nk<_Float16, 16>(mb, p, grid, s) : launch_nk<_Float16, 32>(mb, p, grid, s);
-  if (dt == kBF16) return strip == 16 ? launch_nk<__bf16, 16>(mb, p, grid, s) : launch_nk<__bf16, 32>(mb, p, grid, s);
+  if (dt == kF16) return launch_nk<_Float16>(mb, strip, p, grid, s);
+  if (dt == kBF16) return launch_nk<__bf16>(mb, strip, p, grid, s);
   return hipErrorInvalidValue;
 }
 }  // namespace cmpext3

@@ -213,7 +213,9 @@ struct SkinnyNKShape {
   static_assert(4 * MB * 16 * SW * 4 <= NS * STAGE, "reduction fits the ring");
 };
 
-template <typename T, int MB, int SW, int KS>
+// NT: stream W with the non-temporal policy (W larger than the Infinity Cache would keep
+// for the next call).
+template <typename T, int MB, int SW, int KS, bool NT = false>
 __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p) {
   using S = SkinnyNKShape<MB, SW, KS>;
   constexpr int NS = S::NS;
@@ -263,7 +265,10 @@ __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p)
     const i32x4 ra = make_rsrc_sgpr(Ab + k0);
 #pragma unroll
     for (int i = 0; i < S::W_DMA; ++i)
-      dma_load16(rw, w_k[i] < krem ? w_off[i] : kBufOOB, dst + (wave * S::W_DMA + i) * 1024);
+      if constexpr (NT)
+        dma_load16_stream(rw, w_k[i] < krem ? w_off[i] : kBufOOB, dst + (wave * S::W_DMA + i) * 1024);
+      else
+        dma_load16(rw, w_k[i] < krem ? w_off[i] : kBufOOB, dst + (wave * S::W_DMA + i) * 1024);
 #pragma unroll
     for (int i = 0; i < S::A_DMA; ++i)
       dma_load16(ra, a_k[i] < krem ? a_off[i] : kBufOOB, dst + S::W_BYTES + (wave * S::A_DMA + i) * 1024);

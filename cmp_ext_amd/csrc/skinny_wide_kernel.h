@@ -51,7 +51,9 @@ __device__ __forceinline__ uint32_t wide_off(int k, int seg) {
   return (uint32_t)(k * 256 + ((seg ^ wide_swz(k)) << 5));
 }
 
-template <typename T, int MB>
+// NT: stream B with the non-temporal policy (B larger than the Infinity Cache would keep
+// for the next call).
+template <typename T, int MB, bool NT = false>
 __global__ void __launch_bounds__(256) gemm_skinny_wide_kernel(const GemmParams p, float* ws, int splits,
                                                                int ksplit) {
   using S = WideShape<MB>;
@@ -102,7 +104,10 @@ __global__ void __launch_bounds__(256) gemm_skinny_wide_kernel(const GemmParams 
     const i32x4 ra = make_rsrc_sgpr(Ab + k0);
 #pragma unroll
     for (int i = 0; i < S::B_DMA; ++i)
-      dma_load16(rb, b_k[i] < krem ? b_off[i] : kBufOOB, dst + (wave * S::B_DMA + i) * 1024);
+      if constexpr (NT)
+        dma_load16_stream(rb, b_k[i] < krem ? b_off[i] : kBufOOB, dst + (wave * S::B_DMA + i) * 1024);
+      else
+        dma_load16(rb, b_k[i] < krem ? b_off[i] : kBufOOB, dst + (wave * S::B_DMA + i) * 1024);
 #pragma unroll
     for (int j = 0; j < S::A_HI; ++j)
       if (j < a_cnt)
