@@ -160,13 +160,26 @@ __global__ void __launch_bounds__(256, WAVES) gemm_f32_kernel(const GemmParams p
       }
     }
   }
+  // Stage st's loads.  A stage wholly inside K loads every piece unchecked; only the stage
+  // that holds K's end (and those past it, all zeros) compares each piece's k with K (the
+  // per-piece compare and select on every stage cost 7 %: cfg5 419.5 -> 391.7 us).
   auto load_stage = [&](int st) {
     const int k0 = st * S::BK;
     const int krem = K - k0;
     const uint32_t dst = lds_addr(smem) + (uint32_t)((st % NS) * S::STAGE);
     const i32x4 ra = make_rsrc_sgpr(Abase + k0);
     const i32x4 rb = make_rsrc_sgpr(KN ? Bbase + (int64_t)k0 * ldb : Bbase + k0);
+    const bool whole = krem >= S::BK;  // wave-uniform
     if constexpr (DMA16) {
+      if (whole) {
+#pragma unroll
+        for (int i = 0; i < S::A16; ++i)
+          if (4 * i + wave < S::A_BYTES / 1024) dma_load16(ra, va_off[i], dst + (4 * i + wave) * 1024);
+#pragma unroll
+        for (int i = 0; i < S::B16; ++i)
+          if (4 * i + wave < S::B_BYTES / 1024) dma_load16(rb, vb_off[i], dst + S::A_BYTES + (4 * i + wave) * 1024);
+        return;
+      }
 #pragma unroll
       for (int i = 0; i < S::A16; ++i)
         if (4 * i + wave < S::A_BYTES / 1024)
@@ -176,6 +189,13 @@ __global__ void __launch_bounds__(256, WAVES) gemm_f32_kernel(const GemmParams p
         if (4 * i + wave < S::B_BYTES / 1024)
           dma_load16(rb, vb_k[i] < krem ? vb_off[i] : kBufOOB, dst + S::A_BYTES + (4 * i + wave) * 1024);
     } else {
+      if (whole) {
+#pragma unroll
+        for (int i = 0; i < S::A_DMA; ++i) dma_load4(ra, a_off[i], dst + (wave * S::A_DMA + i) * 256);
+#pragma unroll
+        for (int i = 0; i < S::B_DMA; ++i) dma_load4(rb, b_off[i], dst + S::A_BYTES + (wave * S::B_DMA + i) * 256);
+        return;
+      }
 #pragma unroll
       for (int i = 0; i < S::A_DMA; ++i)
         dma_load4(ra, a_k[i] < krem ? a_off[i] : kBufOOB, dst + (wave * S::A_DMA + i) * 256);

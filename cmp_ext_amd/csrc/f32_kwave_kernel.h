@@ -95,12 +95,31 @@ __global__ void __launch_bounds__(256, BM == 16 ? 4 : 2) gemm_f32_kwave_kernel(c
   }
   unsigned char* ring = smem + wave * (NS * SUB);
   // this wave's j-th step covers k0 = 16 * (4j + wave); steps past K load zeros
+  // (a step wholly inside K loads its pieces unchecked; only the one holding K's end and
+  // those past it compare each piece's k with K)
   auto load_step = [&](int j) {
     const int k0 = BK * (4 * j + wave);
     const int krem = K - k0;
     const uint32_t dst = lds_addr(ring) + (uint32_t)((j % NS) * SUB);
     const i32x4 ra = make_rsrc_sgpr(Abase + k0);
     const i32x4 rb = make_rsrc_sgpr(KN ? Bbase + (int64_t)k0 * ldb : Bbase + k0);
+    if (krem >= BK) {  // wave-uniform
+#pragma unroll
+      for (int t = 0; t < NA; ++t) {
+        if (DMA16)
+          dma_load16(ra, a_off[t], dst + t * 1024);
+        else
+          dma_load4(ra, a_off[t], dst + t * 256);
+      }
+#pragma unroll
+      for (int t = 0; t < NB; ++t) {
+        if (DMA16)
+          dma_load16(rb, b_off[t], dst + A_BYTES + t * 1024);
+        else
+          dma_load4(rb, b_off[t], dst + A_BYTES + t * 256);
+      }
+      return;
+    }
 #pragma unroll
     for (int t = 0; t < NA; ++t) {
       if (DMA16)
