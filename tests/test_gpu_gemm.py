@@ -771,9 +771,14 @@ def test_stream_kernel(dtype, M, N, K, batch, bias):
     c2 = torch.empty_like(c)
     st, call2 = cabi.prepare(CODE[dtype], cabi.B_KN, ag, K, 0, bg, N, K * N, c2, N, M * N, bvg, M, N, K, batch,
                              cabi.BIAS_PER_ROW if bias else 0, 0)
-    assert st == cabi.OK and cabi.run(call2) == cabi.OK
-    torch.cuda.synchronize()
-    assert torch.equal(c, c2)
+    assert st == cabi.OK
+    # repeated back-to-back launches (the ring's waits rely on the order in which a wave's
+    # loads and stores complete): every one bit-identical to the first
+    for _ in range(20):
+        c2.fill_(float("nan"))
+        assert cabi.run(call2) == cabi.OK
+        torch.cuda.synchronize()
+        assert torch.equal(c, c2)
 
 
 def test_every_kernel_family_was_exercised():
