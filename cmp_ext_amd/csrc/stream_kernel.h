@@ -1,5 +1,5 @@
 // Short-K f16/bf16 GEMM over many columns: C[b] = A * B[b] (+ bias per row),
-// M <= 64, K <= 128, B as [K,N] -- the shape of a 1x1 convolution over NCHW
+// M <= 128, K <= 128, B as [K,N] -- the shape of a 1x1 convolution over NCHW
 // activations (A = the weight, shared by every batch entry; B[b] = one image's
 // [C_in][H*W]; C[b] = its [C_out][H*W]); counterpart of the reference's conv2d
 // routed through its GEMM (csrc/main.cpp:402-424).
@@ -9,15 +9,17 @@
 // each CU idle between its tiles' loads (measured 3.9 TB/s).  Here a persistent
 // workgroup per CU walks the 128-column tiles t = blockIdx.x, + gridDim.x, ...
 // (batch entry t / tiles_n) with
-//   * A held in registers for the whole kernel (64 x 128 as MFMA fragments);
+//   * tiles of MT = 64 or 128 rows (all of M) by 128 columns;
+//   * A held in registers for the whole kernel (MT x 128 as MFMA fragments);
 //   * B tiles ([K][128] = 32 KiB, rows of 256 bytes) streamed global -> LDS by
-//     LDS-DMA through a ring of four slots, three tiles in flight;
-//   * per tile 8 MFMAs of 16x16x32 per wave and K/32 sub-steps (4 waves, each
-//     all 64 rows x 32 columns), B fragments by ds_read_b64_tr_b16 as in the
+//     LDS-DMA through a ring of four slots (three for MT = 128, whose results
+//     need twice the staging), three (two) tiles in flight;
+//   * per tile MT/8 MFMAs of 16x16x32 per wave and K/32 sub-steps (4 waves, each
+//     all MT rows x 32 columns), B fragments by ds_read_b64_tr_b16 as in the
 //     tile kernel's [K,N] path;
 //   * the tile's results staged in LDS (row-major, 16-byte chunks XOR-swizzled by
 //     row) and written during the next tile, after its barrier: each wave stores
-//     16 whole rows of 256 bytes with non-temporal 16-byte stores (full cache
+//     MT/4 whole rows of 256 bytes with non-temporal 16-byte stores (full cache
 //     lines that go straight to HBM instead of waiting in L2 as dirty lines;
 //     measured on MI355X for the 64 x 16384 x 128 x 64 convolution: 62.4 us
 //     against 84.5 us for the MFMA layout's 64-byte row pieces through L2, and
@@ -39,20 +41,23 @@ namespace cmpext3 {
 
 constexpr int kStreamN = 128;     // columns per tile
 constexpr int kStreamK = 128;     // largest K (rows of a ring slot)
-constexpr int kStreamSlots = 4;   // ring depth: three tiles in flight while one is read
 // Cache policy of the result stores: non-temporal (the nt bit of the buffer instruction).
 constexpr int kStreamStorePolicy = 2;
 
 // BIAS: 0 none, 2 one value per row of C (the convolution's per-channel bias).
-template <typename T, int BIAS>
+// MT: rows per tile (64 or 128; M <= MT).
+template <typename T, int BIAS, int MT>
 __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p, int total_tiles) {
+  static_assert(MT == 64 || MT == 128, "tile rows");
   constexpr int PITCH = kStreamN * 2;            // bytes per k row of a slot
   constexpr int SLOT = kStreamK * PITCH;         // 32 KiB
   constexpr int P = SLOT / 1024 / 4;             // 1 KiB LDS-DMA loads per wave per tile
-  constexpr int FM = 4, FN = 2, KS = kStreamK / 32;
-  constexpr int Q = FM;                          // 16-byte stores per wave per tile
-  static_assert(2 * P + 2 * Q <= 63, "vmcnt range");
-  constexpr int STG = 64 * 256;                  // one tile's results, two buffers
+  constexpr int FM = MT / 16, FN = 2, KS = kStreamK / 32;
+  constexpr int Q = MT / 16;                     // 16-byte stores per wave per tile (MT/4 rows)
+  constexpr int STG = MT * 256;                  // one tile's results, two buffers
+  constexpr int kStreamSlots = MT == 64 ? 4 : 3;  // ring depth
+  static_assert((kStreamSlots - 2) * (P + Q) <= 63, "vmcnt range");
+  static_assert(kStreamSlots * SLOT + 2 * STG <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[kStreamSlots * SLOT + 2 * STG];
 
   const int tid = threadIdx.x;
@@ -100,7 +105,7 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
     b_n[q] = n;
   }
   const uint32_t lds_w = lds_addr(smem) + (uint32_t)(wave * P * 1024);
-  // Tile i of this workgroup into ring slot i % 4; tiles past the end load through an
+  // Tile i of this workgroup into ring slot i % slots; tiles past the end load through an
   // empty descriptor (no memory read, zeros into LDS) so every iteration issues P loads.
   auto issue = [&](int i) {
     const bool live = i < ntiles;
@@ -128,8 +133,8 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
   // row reads) ----
   const int col = 32 * wave + 16 * (G & 1) + 8 * (G >> 1);
   unsigned char* const stg0 = smem + kStreamSlots * SLOT;
-  // The 4 x 256-byte-row stores of tile i by this wave (rows 16 wave .. +15, an empty
-  // descriptor when there is no tile i): always Q instructions.
+  // The Q stores of 4 x 256-byte rows of tile i by this wave (rows MT/4 wave .. +MT/4-1, an
+  // empty descriptor when there is no tile i): always Q instructions.
   auto store = [&](int i) {
     const bool live = i >= 0 && i < ntiles;
     const int t = live ? me + i * step : 0;
@@ -142,12 +147,12 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
     u32x4 v[Q];
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
-      const int row = 16 * wave + 4 * q + (lane >> 4);
+      const int row = (MT / 4) * wave + 4 * q + (lane >> 4);
       v[q] = *(const u32x4*)(stg + row * 256 + ((ch ^ (row & 15)) << 4));
     }
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
-      const int row = 16 * wave + 4 * q + (lane >> 4);
+      const int row = (MT / 4) * wave + 4 * q + (lane >> 4);
       const uint32_t off = (col_ok && row < M) ? (uint32_t)(row * p.ldc + 8 * ch) * 2u : kBufOOB;
       __builtin_amdgcn_raw_buffer_store_b128(v[q], rc, off, 0, kStreamStorePolicy);
     }
@@ -155,15 +160,16 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
 
   static_for<kStreamSlots - 1>([&](auto ic) { issue(decltype(ic)::value); });
   for (int i = 0; i < ntiles; ++i) {
-    // Tile i landed: after its loads (issued in iteration i-3) this wave issued the
-    // stores and loads of two more iterations (2P + 2Q instructions; 2P + Q and 2P
-    // for i = 1, 0), and vector-memory instructions complete in issue order.
-    if (i >= 2)
-      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(2 * P + 2 * Q) : "memory");
+    // Tile i landed: after its loads (issued in iteration i - (slots-1), or before the
+    // loop) this wave issued the stores and loads of slots-2 more iterations ((slots-2) x
+    // (P + Q) instructions; fewer stores, but at least (slots-2) x P loads, in the first
+    // iterations), and vector-memory instructions complete in issue order.
+    if (i >= kStreamSlots - 2)
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"((kStreamSlots - 2) * (P + Q)) : "memory");
     else
-      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(2 * P) : "memory");
-    // every wave is past tile i-1's reads (its slot takes tile i+3) and has staged
-    // tile i-1's results
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"((kStreamSlots - 2) * P) : "memory");
+    // every wave is past tile i-1's reads (its slot takes tile i + slots-1) and has
+    // staged tile i-1's results
     store(i - 1);
     issue(i + kStreamSlots - 1);
 

@@ -49,7 +49,8 @@ SHAPES = [(2, 256, 32, 32, 512), (2, 512, 64, 64, 16), (1, 64, 7, 7, 96), (3, 40
           (1, 320, 64, 64, 320), (4, 128, 16, 16, 1), (1, 1, 8, 8, 8),
           (16, 128, 64, 64, 64), (64, 128, 32, 32, 40),  # few output channels, many pixels: tiled
           (4, 129, 31, 33, 200),  # odd channels and pixels: weight and images copied zero-padded
-          (8, 64, 256, 256, 48)]  # 4096 column tiles of 128 pixels: the streaming kernel
+          (8, 64, 256, 256, 48),  # 4096 column tiles of 128 pixels: the streaming kernel
+          (8, 96, 256, 256, 128)]  # ... with 128-row tiles
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])

@@ -25,7 +25,8 @@ CODE = {"fp16": cabi.F16, "bf16": cabi.BF16, "fp32": cabi.F32}
 MATMUL = {"fp16": cmpext3.fp16_matmul, "bf16": cmpext3.bf16_matmul, "fp32": cmpext3.fp32_matmul}
 KERNEL_NAMES = ["tile256x256", "tile256x224", "tile128x128", "tile64x256", "skinny", "skinny_wide", "skinny_nk",
                 "f32tile128x128",
-                "f32tile64x64", "f32tile96x64", "f32tile64x64k4", "f32tile16x64k4", "generic64x64", "stream64x128"]
+                "f32tile64x64", "f32tile96x64", "f32tile64x64k4", "f32tile16x64k4", "generic64x64", "stream64x128",
+                "stream128x128"]
 SEEN_KERNELS = set()
 
 
@@ -736,6 +737,8 @@ def test_tiled_split_k_batched(dtype):
     (64, 8200, 128, 64, False),   # 65 column tiles per entry, the last one 8 columns wide
     (40, 16384, 72, 32, True),    # ragged M and K, bias per row (4096 tiles: 16 per CU)
     (1, 524288, 8, 1, False),     # one row, K = 8, one product of 4096 tiles
+    (128, 16384, 128, 32, True),  # 128-row tiles
+    (96, 8200, 64, 64, False),    # 128-row tiles, M and N ragged
 ])
 def test_stream_kernel(dtype, M, N, K, batch, bias):
     """Short-K products over many columns with one A for the whole batch (the 1x1
@@ -754,7 +757,7 @@ def test_stream_kernel(dtype, M, N, K, batch, bias):
     assert st == cabi.OK
     _, desc = cabi.describe(call)
     SEEN_KERNELS.add(kernel_of(desc))
-    assert kernel_of(desc) == "stream64x128", desc
+    assert kernel_of(desc) == ("stream64x128" if M <= 64 else "stream128x128"), desc
     assert cabi.run(call) == cabi.OK
     torch.cuda.synchronize()
     assert not torch.isnan(c).any()

@@ -4,7 +4,7 @@ import pytest
 from cmp_ext_amd import cabi
 
 K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKINNY_WIDE, K_F32_96, K_TILE64, \
-    K_SKINNY_NK, K_F32_64K4, K_F32_16K4, K_STREAM = range(14)
+    K_SKINNY_NK, K_F32_64K4, K_F32_16K4, K_STREAM, K_STREAM128 = range(15)
 
 
 @pytest.mark.parametrize("dtype,M,N,K,expect", [
@@ -75,7 +75,10 @@ def test_stream_kernel_for_convolution_shapes():
     # batch entry, a bias per column, a misaligned A, or rows of C not 16-byte multiples
     assert _prepared_kernel(cabi.F16, 64, 16384, 128, 31, 0)[0] != K_STREAM
     assert _prepared_kernel(cabi.F16, 64, 16384, 136, 64, 0)[0] != K_STREAM
-    assert _prepared_kernel(cabi.F16, 65, 16384, 128, 64, 0)[0] != K_STREAM
+    kid, desc = _prepared_kernel(cabi.F16, 65, 16384, 128, 64, 0)
+    assert kid == K_STREAM128 and "tile=128x128" in desc, desc   # 65..128 rows: 128-row tiles
+    assert _prepared_kernel(cabi.BF16, 128, 16384, 128, 64, 0, cabi.BIAS_PER_ROW, bias=0x1000)[0] == K_STREAM128
+    assert _prepared_kernel(cabi.F16, 129, 16384, 128, 64, 0)[0] not in (K_STREAM, K_STREAM128)
     assert _prepared_kernel(cabi.F16, 64, 16384, 128, 64, 64 * 128)[0] != K_STREAM
     assert _prepared_kernel(cabi.F16, 64, 16384, 128, 64, 0, 0, bias=0x1000)[0] != K_STREAM
     assert _prepared_kernel(cabi.F16, 64, 16384, 128, 64, 0, align=8)[0] != K_STREAM
