@@ -44,8 +44,8 @@ enum KernelId : int {
   kSkinnyNK = 10,     // f16/bf16, M <= 64, B is [N,K]: 16- or 32-row strips of W, all of K per workgroup
   kF32Tile64K4 = 11,  // fp32, 64x64 tile, K split over the workgroup's four waves (few tiles per CU)
   kF32Tile16K4 = 12,  // same with 16x64 tiles (M <= 16)
-  kStream64x128 = 13, // f16/bf16, M <= 64, K <= 128, B is [K,N]: persistent workgroups stream 128-column tiles
-  kStream128x128 = 14,  // same with 128-row tiles (64 < M <= 128)
+  kStream64x128 = 13, // f16/bf16, M <= 64, K <= 256, B is [K,N]: persistent workgroups stream 128-column tiles
+  kStream128x128 = 14,  // same with 128-row tiles (64 < M <= 128, K <= 128)
   kNumKernels = 15
 };
 

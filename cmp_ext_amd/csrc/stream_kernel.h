@@ -1,35 +1,36 @@
 // Short-K f16/bf16 GEMM over many columns: C[b] = A * B[b] (+ bias per row),
-// M <= 128, K <= 128, B as [K,N] -- the shape of a 1x1 convolution over NCHW
-// activations (A = the weight, shared by every batch entry; B[b] = one image's
-// [C_in][H*W]; C[b] = its [C_out][H*W]); counterpart of the reference's conv2d
-// routed through its GEMM (csrc/main.cpp:402-424).
+// M <= 128 and K <= 128, or M <= 64 and K <= 256, B as [K,N] -- the shape of a
+// 1x1 convolution over NCHW activations (A = the weight, shared by every batch
+// entry; B[b] = one image's [C_in][H*W]; C[b] = its [C_out][H*W]); counterpart
+// of the reference's conv2d routed through its GEMM (csrc/main.cpp:402-424).
 //
 // Such a product moves ~3 bytes per 64 flops: it is bound by streaming B in and
 // C out, and a tile kernel that holds one 64 x 256 tile per workgroup leaves
 // each CU idle between its tiles' loads (measured 3.9 TB/s).  Here a persistent
 // workgroup per CU walks the 128-column tiles t = blockIdx.x, + gridDim.x, ...
 // (batch entry t / tiles_n) with
-//   * tiles of MT = 64 or 128 rows (all of M) by 128 columns;
-//   * A held in registers for the whole kernel (MT x 128 as MFMA fragments);
-//   * B tiles ([K][128] = 32 KiB, rows of 256 bytes) streamed global -> LDS by
+//   * tiles of MT = 64 or 128 rows (all of M) by 128 columns, each read as KC = 1
+//     or 2 chunks of 128 k-rows (K <= 128 KC; KC = 2 only with MT = 64);
+//   * A held in registers for the whole kernel (MT x 128 KC as MFMA fragments);
+//   * B chunks ([128][128] = 32 KiB, rows of 256 bytes) streamed global -> LDS by
 //     LDS-DMA through a ring of four slots (three for MT = 128, whose results
-//     need twice the staging), three (two) tiles in flight;
-//   * per tile MT/8 MFMAs of 16x16x32 per wave and K/32 sub-steps (4 waves, each
-//     all MT rows x 32 columns), B fragments by ds_read_b64_tr_b16 as in the
+//     need twice the staging), three (two) chunks in flight;
+//   * per chunk MT/8 MFMAs of 16x16x32 per wave and 4 sub-steps of 32 k (4 waves,
+//     each all MT rows x 32 columns), B fragments by ds_read_b64_tr_b16 as in the
 //     tile kernel's [K,N] path;
 //   * the tile's results staged in LDS (row-major, 16-byte chunks XOR-swizzled by
-//     row) and written during the next tile, after its barrier: each wave stores
-//     MT/4 whole rows of 256 bytes with non-temporal 16-byte stores (full cache
-//     lines that go straight to HBM instead of waiting in L2 as dirty lines;
-//     measured on MI355X for the 64 x 16384 x 128 x 64 convolution: 62.4 us
-//     against 84.5 us for the MFMA layout's 64-byte row pieces through L2, and
+//     row) and written during the next tile's chunks, after their barriers: each
+//     wave stores MT/4 whole rows of 256 bytes with non-temporal 16-byte stores
+//     (full cache lines that go straight to HBM instead of waiting in L2 as dirty
+//     lines; measured on MI355X for the 64 x 16384 x 128 x 64 convolution: 62.4
+//     us against 84.5 us for the MFMA layout's 64-byte row pieces through L2, and
 //     72.3 us for those pieces non-temporal), out-of-range lanes masked by the
-//     descriptor, so that every iteration issues the same number of
-//     vector-memory instructions and one "s_waitcnt vmcnt" constant certifies
-//     the tile about to be read.
-// Requirements (checked by the selector): K <= 128 and K, N, lda, ldb, ldc
-// multiples of 8; A, B and C 16-byte aligned; one A for the whole batch
-// (batch 1 or stride_a 0); 64 * ldc * 2 and 128 * ldb * 2 below 2^31.
+//     descriptor, spread evenly over the tile's KC chunks, so that every chunk
+//     issues the same number of vector-memory instructions and one
+//     "s_waitcnt vmcnt" constant certifies the chunk about to be read.
+// Requirements (checked by the selector): K, N, lda, ldb, ldc multiples of 8;
+// A, B and C 16-byte aligned; one A for the whole batch (batch 1 or stride_a 0);
+// 128 * ldb * 2 and 128 * ldc * 2 below 2^31.
 #pragma once
 
 #include <type_traits>
@@ -40,25 +41,28 @@
 namespace cmpext3 {
 
 constexpr int kStreamN = 128;     // columns per tile
-constexpr int kStreamK = 128;     // largest K (rows of a ring slot)
+constexpr int kStreamKC = 128;    // k rows per chunk (rows of a ring slot)
 // Cache policy of the result stores: non-temporal (the nt bit of the buffer instruction).
 constexpr int kStreamStorePolicy = 2;
 
 // BIAS: 0 none, 2 one value per row of C (the convolution's per-channel bias).
-// MT: rows per tile (64 or 128; M <= MT).
-template <typename T, int BIAS, int MT>
+// MT: rows per tile (M <= MT); KC: chunks of 128 k per tile (K <= 128 KC).
+// NT: B read with the non-temporal cache policy (for read-dominated products).
+template <typename T, int BIAS, int MT, int KC, bool NT>
 __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p, int total_tiles) {
-  static_assert(MT == 64 || MT == 128, "tile rows");
+  static_assert((MT == 64 && (KC == 1 || KC == 2)) || (MT == 128 && KC == 1), "tile shapes");
   constexpr int PITCH = kStreamN * 2;            // bytes per k row of a slot
-  constexpr int SLOT = kStreamK * PITCH;         // 32 KiB
-  constexpr int P = SLOT / 1024 / 4;             // 1 KiB LDS-DMA loads per wave per tile
-  constexpr int FM = MT / 16, FN = 2, KS = kStreamK / 32;
+  constexpr int SLOT = kStreamKC * PITCH;        // 32 KiB
+  constexpr int P = SLOT / 1024 / 4;             // 1 KiB LDS-DMA loads per wave per chunk
+  constexpr int FM = MT / 16, FN = 2, KSC = kStreamKC / 32, KS = KSC * KC;
   constexpr int Q = MT / 16;                     // 16-byte stores per wave per tile (MT/4 rows)
+  constexpr int QC = Q / KC;                     // ... per chunk
   constexpr int STG = MT * 256;                  // one tile's results, two buffers
-  constexpr int kStreamSlots = MT == 64 ? 4 : 3;  // ring depth
-  static_assert((kStreamSlots - 2) * (P + Q) <= 63, "vmcnt range");
-  static_assert(kStreamSlots * SLOT + 2 * STG <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[kStreamSlots * SLOT + 2 * STG];
+  constexpr int SLOTS = MT == 64 ? 4 : 3;        // ring depth (chunks)
+  static_assert(Q % KC == 0, "stores spread evenly over the chunks");
+  static_assert((SLOTS - 2) * (P + QC) <= 63, "vmcnt range");
+  static_assert(SLOTS * SLOT + 2 * STG <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[SLOTS * SLOT + 2 * STG];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -68,6 +72,7 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
   const int tiles_n = p.tiles_n;
   const int me = blockIdx.x, step = gridDim.x;
   const int ntiles = total_tiles > me ? (total_tiles - me + step - 1) / step : 0;
+  const int nchunks = ntiles * KC;
 
   // ---- A fragments (rows 16i + r16, k = 32s + 8G .. +7), zero past M and K ----
   u32x4 fa[FM][KS];
@@ -94,30 +99,38 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
 #pragma unroll
   for (int i = 0; i < FM; ++i) asm volatile("" : "+v"(bias_m[i]));
 
-  // ---- DMA: piece q of wave w fills bytes (w*P + q) KiB of a slot = k rows 4(wP+q) .. +3 ----
-  uint32_t b_off[P];
+  // ---- DMA: piece q of wave w fills bytes (w*P + q) KiB of a slot = k rows 4(wP+q) .. +3
+  // of the chunk ----
+  // b_off[h][q]: the piece's offset in chunk h of a tile, or kBufOOB past K
+  uint32_t b_off[KC][P];
   int b_n[P];
 #pragma unroll
   for (int q = 0; q < P; ++q) {
     int k, n;
     dma_kn_geom(wave * P + q, lane, PITCH, k, n);
-    b_off[q] = k < K ? (uint32_t)(k * p.ldb + n) * 2u : kBufOOB;
+#pragma unroll
+    for (int h = 0; h < KC; ++h) b_off[h][q] = kStreamKC * h + k < K ? (uint32_t)(k * p.ldb + n) * 2u : kBufOOB;
     b_n[q] = n;
   }
   const uint32_t lds_w = lds_addr(smem) + (uint32_t)(wave * P * 1024);
-  // Tile i of this workgroup into ring slot i % slots; tiles past the end load through an
-  // empty descriptor (no memory read, zeros into LDS) so every iteration issues P loads.
-  auto issue = [&](int i) {
-    const bool live = i < ntiles;
-    const int t = live ? me + i * step : 0;
+  // Chunk c = KC i + h (tile i, its k rows from 128 h; h known at compile time) of this
+  // workgroup into ring slot c % SLOTS; chunks past the end load through an empty
+  // descriptor (no memory read, zeros into LDS) so every iteration issues P loads.
+  auto issue = [&](int c, auto hc) {
+    constexpr int h = decltype(hc)::value;
+    const bool live = c < nchunks;
+    const int t = live ? me + (c / KC) * step : 0;
     const int bz = t / tiles_n, n0 = (t - bz * tiles_n) * kStreamN;
-    i32x4 r = make_rsrc_sgpr((const T*)p.B + (int64_t)bz * p.stride_b + n0);
+    i32x4 r = make_rsrc_sgpr((const T*)p.B + (int64_t)bz * p.stride_b + (int64_t)(kStreamKC * h) * p.ldb + n0);
     r[2] = live ? (int)kBufRecords : 0;
-    const uint32_t base = lds_w + (uint32_t)((i % kStreamSlots) * SLOT);
+    const uint32_t base = lds_w + (uint32_t)((c % SLOTS) * SLOT);
     static_for<P>([&](auto qc) {
       constexpr int q = decltype(qc)::value;
-      const uint32_t voff = n0 + b_n[q] < N ? b_off[q] : kBufOOB;
-      dma_load16_m0(r, voff, 0u, base, std::integral_constant<uint32_t, (uint32_t)(q * 1024)>{});
+      const uint32_t voff = n0 + b_n[q] < N ? b_off[h][q] : kBufOOB;
+      if constexpr (NT)
+        dma_load16_stream(r, voff, base + (uint32_t)(q * 1024));
+      else
+        dma_load16_m0(r, voff, 0u, base, std::integral_constant<uint32_t, (uint32_t)(q * 1024)>{});
     });
   };
 
@@ -132,10 +145,12 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
   // col/8 of the row, at chunk position (col/8) ^ (row % 16) (conflict-free writes and
   // row reads) ----
   const int col = 32 * wave + 16 * (G & 1) + 8 * (G >> 1);
-  unsigned char* const stg0 = smem + kStreamSlots * SLOT;
-  // The Q stores of 4 x 256-byte rows of tile i by this wave (rows MT/4 wave .. +MT/4-1, an
-  // empty descriptor when there is no tile i): always Q instructions.
-  auto store = [&](int i) {
+  unsigned char* const stg0 = smem + SLOTS * SLOT;
+  // Part `part` of KC of this wave's stores of tile i: QC stores of 4 x 256-byte rows
+  // (rows MT/4 wave + 4 QC part .. of the wave's MT/4 rows; an empty descriptor when there
+  // is no tile i): always QC instructions.
+  auto store = [&](int i, auto partc) {
+    constexpr int part = decltype(partc)::value;
     const bool live = i >= 0 && i < ntiles;
     const int t = live ? me + i * step : 0;
     const int bz = t / tiles_n, n0 = (t - bz * tiles_n) * kStreamN;
@@ -144,62 +159,70 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
     const unsigned char* stg = stg0 + (i & 1) * STG;
     const int ch = lane & 15;
     const bool col_ok = n0 + 8 * ch < N;
-    u32x4 v[Q];
+    u32x4 v[QC];
 #pragma unroll
-    for (int q = 0; q < Q; ++q) {
-      const int row = (MT / 4) * wave + 4 * q + (lane >> 4);
+    for (int q = 0; q < QC; ++q) {
+      const int row = (MT / 4) * wave + 4 * (QC * part + q) + (lane >> 4);
       v[q] = *(const u32x4*)(stg + row * 256 + ((ch ^ (row & 15)) << 4));
     }
 #pragma unroll
-    for (int q = 0; q < Q; ++q) {
-      const int row = (MT / 4) * wave + 4 * q + (lane >> 4);
+    for (int q = 0; q < QC; ++q) {
+      const int row = (MT / 4) * wave + 4 * (QC * part + q) + (lane >> 4);
       const uint32_t off = (col_ok && row < M) ? (uint32_t)(row * p.ldc + 8 * ch) * 2u : kBufOOB;
       __builtin_amdgcn_raw_buffer_store_b128(v[q], rc, off, 0, kStreamStorePolicy);
     }
   };
 
-  static_for<kStreamSlots - 1>([&](auto ic) { issue(decltype(ic)::value); });
+  static_for<SLOTS - 1>([&](auto cc) {
+    constexpr int c = decltype(cc)::value;
+    issue(c, std::integral_constant<int, c % KC>{});
+  });
   for (int i = 0; i < ntiles; ++i) {
-    // Tile i landed: after its loads (issued in iteration i - (slots-1), or before the
-    // loop) this wave issued the stores and loads of slots-2 more iterations ((slots-2) x
-    // (P + Q) instructions; fewer stores, but at least (slots-2) x P loads, in the first
-    // iterations), and vector-memory instructions complete in issue order.
-    if (i >= kStreamSlots - 2)
-      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"((kStreamSlots - 2) * (P + Q)) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"((kStreamSlots - 2) * P) : "memory");
-    // every wave is past tile i-1's reads (its slot takes tile i + slots-1) and has
-    // staged tile i-1's results
-    store(i - 1);
-    issue(i + kStreamSlots - 1);
-
-    const unsigned char* sb = smem + (i % kStreamSlots) * SLOT;
-    u32x4 fb[KS][FN];
-    static_for<KS * FN * 2>([&](auto rc) {
-      constexpr int r = decltype(rc)::value, s = r / (2 * FN), j = (r / 2) % FN, half = r % 2;
-      typedef short s16x4 __attribute__((ext_vector_type(4)));
-      const unsigned char* q = sb + fb_off[j] + (32 * s + 4 * half) * PITCH;
-      const u32x2 v = __builtin_bit_cast(
-          u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q));
-      if constexpr (half == 0) {
-        fb[s][j].x = v.x;
-        fb[s][j].y = v.y;
-      } else {
-        fb[s][j].z = v.x;
-        fb[s][j].w = v.y;
-      }
-    });
     f32x4 acc[FM][FN];
     static_for<FM * FN>([&](auto xc) {
       constexpr int x = decltype(xc)::value;
       acc[x / FN][x % FN] = f32x4{0.f, 0.f, 0.f, 0.f};
     });
-    static_for<KS * FM * FN>([&](auto xc) {
-      constexpr int x = decltype(xc)::value, s = x / (FM * FN), i = (x / FN) % FM, j = x % FN;
-      acc[i][j] = Mfma<T>::mma(fb[s][j], fa[i][s], acc[i][j]);
+    static_for<KC>([&](auto hc) {
+      constexpr int h = decltype(hc)::value;
+      const int c = i * KC + h;
+      // Chunk c landed: after its loads (issued in iteration c - (SLOTS-1), or before the
+      // loop) this wave issued the stores and loads of SLOTS-2 more iterations ((SLOTS-2) x
+      // (P + QC) instructions; at least (SLOTS-2) x P in the first iterations, where the
+      // loads of later chunks came before the loop), and vector-memory instructions
+      // complete in issue order.
+      if (c >= SLOTS - 2)
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"((SLOTS - 2) * (P + QC)) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"((SLOTS - 2) * P) : "memory");
+      // every wave is past chunk c-1's reads (its slot takes chunk c + SLOTS-1) and has
+      // staged tile i-1's results
+      store(i - 1, hc);
+      issue(c + SLOTS - 1, std::integral_constant<int, (h + SLOTS - 1) % KC>{});
+
+      const unsigned char* sb = smem + (c % SLOTS) * SLOT;
+      u32x4 fb[KSC][FN];
+      static_for<KSC * FN * 2>([&](auto rc) {
+        constexpr int r = decltype(rc)::value, s = r / (2 * FN), j = (r / 2) % FN, half = r % 2;
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        const unsigned char* q = sb + fb_off[j] + (32 * s + 4 * half) * PITCH;
+        const u32x2 v = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q));
+        if constexpr (half == 0) {
+          fb[s][j].x = v.x;
+          fb[s][j].y = v.y;
+        } else {
+          fb[s][j].z = v.x;
+          fb[s][j].w = v.y;
+        }
+      });
+      static_for<KSC * FM * FN>([&](auto xc) {
+        constexpr int x = decltype(xc)::value, s = x / (FM * FN), ii = (x / FN) % FM, j = x % FN;
+        acc[ii][j] = Mfma<T>::mma(fb[s][j], fa[ii][KSC * h + s], acc[ii][j]);
+      });
     });
-    // results -> staging buffer i % 2, last read by the stores of tile i-2 (iteration
-    // i-1), which every wave finished before this iteration's barrier
+    // results -> staging buffer i % 2, last read by the stores of tile i-2 (during the
+    // chunks of tile i-1), which every wave finished before this tile's barriers
     unsigned char* stg = stg0 + (i & 1) * STG;
 #pragma unroll
     for (int ii = 0; ii < FM; ++ii) {
@@ -224,7 +247,7 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
     }
   }
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");  // the last tile is staged
-  store(ntiles - 1);
+  static_for<KC>([&](auto hc) { store(ntiles - 1, hc); });
   asm volatile("s_waitcnt vmcnt(0)" : : : "memory");  // no LDS DMA may outlive the workgroup
 }
 

@@ -739,6 +739,9 @@ def test_tiled_split_k_batched(dtype):
     (1, 524288, 8, 1, False),     # one row, K = 8, one product of 4096 tiles
     (128, 16384, 128, 32, True),  # 128-row tiles
     (96, 8200, 64, 64, False),    # 128-row tiles, M and N ragged
+    (64, 16384, 256, 32, True),   # K = 256: two chunks of 128 k per tile
+    (48, 8200, 200, 64, False),   # second chunk ragged (72 k), M and N ragged
+    (8, 131072, 136, 4, True),    # second chunk of 8 k
 ])
 def test_stream_kernel(dtype, M, N, K, batch, bias):
     """Short-K products over many columns with one A for the whole batch (the 1x1
