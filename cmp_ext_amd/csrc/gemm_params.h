@@ -45,7 +45,7 @@ enum KernelId : int {
   kF32Tile64K4 = 11,  // fp32, 64x64 tile, K split over the workgroup's four waves (few tiles per CU)
   kF32Tile16K4 = 12,  // same with 16x64 tiles (M <= 16)
   kStream64x128 = 13, // f16/bf16, M <= 64, K <= 256, B is [K,N]: persistent workgroups stream 128-column tiles
-  kStream128x128 = 14,  // same with 128-row tiles (64 < M <= 128, K <= 128)
+  kStream128x128 = 14,  // same with 128-row tiles (64 < M <= 128)
   kNumKernels = 15
 };
 

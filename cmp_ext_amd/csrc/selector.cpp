@@ -222,7 +222,7 @@ int make_plan_core(const Request& r, Plan* plan) {
         p.kernel = kSkinny;
         p.bn = 32;
       }
-    } else if (fast && r.layout == kKN && r.M <= 128 && r.K <= (r.M <= 64 ? 256 : 128) && r.N % 8 == 0 && r.ldc % 8 == 0 &&
+    } else if (fast && r.layout == kKN && r.M <= 128 && r.K <= 256 && r.N % 8 == 0 && r.ldc % 8 == 0 &&
                (!batched || (r.stride_a == 0 && r.stride_c % 8 == 0)) && (!r.has_bias || r.bias_row) &&
                128 * r.ldb * 2 <= kIntMax && 128 * r.ldc * 2 <= kIntMax &&
                cdiv(r.N, 128) * r.batch >= 16 * kNumCUs && cdiv(r.N, 128) * r.batch <= kIntMax) {

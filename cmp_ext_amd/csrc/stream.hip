@@ -1,5 +1,5 @@
-// Launcher of the short-K streaming kernel (f16/bf16; M <= 128 with K <= 128, or M <= 64
-// with K <= 256; bias none or per row).
+// Launcher of the short-K streaming kernel (f16/bf16, M <= 128, K <= 256, bias none or per
+// row).
 #include "kernels.h"
 #include "selector.h"
 #include "stream_kernel.h"
@@ -13,22 +13,33 @@ namespace cmpext3 {
 // 16 <- 128 51.7 / 57.8, 32 <- 64 37.5 / 38.0.
 static bool stream_nt(const GemmParams& p) { return p.K >= 160; }
 
-template <typename T, int MT, int KC, bool NT>
+template <typename T, int WG, int KC, bool NT>
 static void launch_stream_t(const GemmParams& p, int total, unsigned wgs, hipStream_t s) {
   if (p.bias != nullptr)
-    hipLaunchKernelGGL((gemm_stream_kernel<T, 2, MT, KC, NT>), dim3(wgs), dim3(256), 0, s, p, total);
+    hipLaunchKernelGGL((gemm_stream_kernel<T, 2, WG, KC, NT>), dim3(wgs), dim3(256 * WG), 0, s, p, total);
   else
-    hipLaunchKernelGGL((gemm_stream_kernel<T, 0, MT, KC, NT>), dim3(wgs), dim3(256), 0, s, p, total);
+    hipLaunchKernelGGL((gemm_stream_kernel<T, 0, WG, KC, NT>), dim3(wgs), dim3(256 * WG), 0, s, p, total);
 }
 
+template <typename T, int WG>
+static void launch_stream_rows(const GemmParams& p, int total, unsigned wgs, hipStream_t s) {
+  if (p.K <= kStreamKC)
+    launch_stream_t<T, WG, 1, false>(p, total, wgs, s);
+  else if (stream_nt(p))
+    launch_stream_t<T, WG, 2, true>(p, total, wgs, s);
+  else
+    launch_stream_t<T, WG, 2, false>(p, total, wgs, s);
+}
+
+// 65..128 rows: two groups of 4 waves, 64 rows each (MI355X, 64 images of 128 x 128
+// pixels, against one group of 4 waves of 128 rows each: 128 <- 128 channels 85.3 ->
+// 83.6 us, 128 <- 64 63.7 -> 61.1 us, 72 <- 32 59.7 -> 51.5 us; and K up to 256 fits).
 template <typename T>
 static void launch_stream_shape(const GemmParams& p, int total, unsigned wgs, hipStream_t s) {
   if (p.M > 64)
-    launch_stream_t<T, 128, 1, false>(p, total, wgs, s);
-  else if (p.K > kStreamKC)
-    stream_nt(p) ? launch_stream_t<T, 64, 2, true>(p, total, wgs, s) : launch_stream_t<T, 64, 2, false>(p, total, wgs, s);
+    launch_stream_rows<T, 2>(p, total, wgs, s);
   else
-    launch_stream_t<T, 64, 1, false>(p, total, wgs, s);
+    launch_stream_rows<T, 1>(p, total, wgs, s);
 }
 
 hipError_t launch_stream(DType dt, const GemmParams& p, dim3 grid, hipStream_t s) {
@@ -36,8 +47,7 @@ hipError_t launch_stream(DType dt, const GemmParams& p, dim3 grid, hipStream_t s
   // workgroup per CU walks all of them
   const int64_t total = (int64_t)grid.x * grid.z;
   if (total <= 0) return hipSuccess;
-  if (total > 0x7FFFFFFF || (p.bias != nullptr && !p.bias_row) || p.M > 128 ||
-      p.K > (p.M > 64 ? 1 : 2) * kStreamKC)
+  if (total > 0x7FFFFFFF || (p.bias != nullptr && !p.bias_row) || p.M > 128 || p.K > 2 * kStreamKC)
     return hipErrorInvalidValue;
   const unsigned wgs = (unsigned)std::min<int64_t>(total, kNumCUs);
   if (dt == kF16)

@@ -1,26 +1,28 @@
 // Short-K f16/bf16 GEMM over many columns: C[b] = A * B[b] (+ bias per row),
-// M <= 128 and K <= 128, or M <= 64 and K <= 256, B as [K,N] -- the shape of a
-// 1x1 convolution over NCHW activations (A = the weight, shared by every batch
-// entry; B[b] = one image's [C_in][H*W]; C[b] = its [C_out][H*W]); counterpart
-// of the reference's conv2d routed through its GEMM (csrc/main.cpp:402-424).
+// M <= 128 and K <= 256, B as [K,N] -- the shape of a 1x1 convolution over NCHW
+// activations (A = the weight, shared by every batch entry; B[b] = one image's
+// [C_in][H*W]; C[b] = its [C_out][H*W]); counterpart of the reference's conv2d
+// routed through its GEMM (csrc/main.cpp:402-424).
 //
 // Such a product moves ~3 bytes per 64 flops: it is bound by streaming B in and
 // C out, and a tile kernel that holds one 64 x 256 tile per workgroup leaves
 // each CU idle between its tiles' loads (measured 3.9 TB/s).  Here a persistent
 // workgroup per CU walks the 128-column tiles t = blockIdx.x, + gridDim.x, ...
 // (batch entry t / tiles_n) with
-//   * tiles of MT = 64 or 128 rows (all of M) by 128 columns, each read as KC = 1
-//     or 2 chunks of 128 k-rows (K <= 128 KC; KC = 2 only with MT = 64);
-//   * A held in registers for the whole kernel (MT x 128 KC as MFMA fragments);
+//   * tiles of MT = 64 WG rows (all of M) by 128 columns, WG = 1 or 2 groups of 4 waves,
+//     group g computing rows 64 g .. 64 g + 63; each tile read as KC = 1 or 2 chunks of
+//     128 k-rows (K <= 128 KC);
+//   * A held in registers for the whole kernel (each wave its 64 rows x 128 KC as MFMA
+//     fragments);
 //   * B chunks ([128][128] = 32 KiB, rows of 256 bytes) streamed global -> LDS by
 //     LDS-DMA through a ring of four slots (three for MT = 128, whose results
 //     need twice the staging), three (two) chunks in flight;
-//   * per chunk MT/8 MFMAs of 16x16x32 per wave and 4 sub-steps of 32 k (4 waves,
-//     each all MT rows x 32 columns), B fragments by ds_read_b64_tr_b16 as in the
-//     tile kernel's [K,N] path;
+//   * per chunk and wave (its rows x 32 columns; the 4 waves of a group split the
+//     128 columns) 4 sub-steps of 32 k on 16x16x32 MFMAs, B fragments by
+//     ds_read_b64_tr_b16 as in the tile kernel's [K,N] path;
 //   * the tile's results staged in LDS (row-major, 16-byte chunks XOR-swizzled by
 //     row) and written during the next tile's chunks, after their barriers: each
-//     wave stores MT/4 whole rows of 256 bytes with non-temporal 16-byte stores
+//     wave stores MT/waves whole rows of 256 bytes with non-temporal 16-byte stores
 //     (full cache lines that go straight to HBM instead of waiting in L2 as dirty
 //     lines; measured on MI355X for the 64 x 16384 x 128 x 64 convolution: 62.4
 //     us against 84.5 us for the MFMA layout's 64-byte row pieces through L2, and
@@ -46,16 +48,20 @@ constexpr int kStreamKC = 128;    // k rows per chunk (rows of a ring slot)
 constexpr int kStreamStorePolicy = 2;
 
 // BIAS: 0 none, 2 one value per row of C (the convolution's per-channel bias).
-// MT: rows per tile (M <= MT); KC: chunks of 128 k per tile (K <= 128 KC).
+// WG: groups of 4 waves, group g computing rows 64 g .. 64 g + 63 of the tile (MT = 64 WG
+// rows, M <= MT); KC: chunks of 128 k per tile (K <= 128 KC).
 // NT: B read with the non-temporal cache policy (for read-dominated products).
-template <typename T, int BIAS, int MT, int KC, bool NT>
-__global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p, int total_tiles) {
-  static_assert((MT == 64 && (KC == 1 || KC == 2)) || (MT == 128 && KC == 1), "tile shapes");
+template <typename T, int BIAS, int WG, int KC, bool NT>
+__global__ void __launch_bounds__(256 * WG, 1) gemm_stream_kernel(const GemmParams p, int total_tiles) {
+  static_assert((WG == 1 || WG == 2) && (KC == 1 || KC == 2), "tile shapes");
+  constexpr int RW = 64;                         // rows per wave
+  constexpr int MT = RW * WG;                    // rows per tile
+  constexpr int NW = 4 * WG;                     // waves
   constexpr int PITCH = kStreamN * 2;            // bytes per k row of a slot
   constexpr int SLOT = kStreamKC * PITCH;        // 32 KiB
-  constexpr int P = SLOT / 1024 / 4;             // 1 KiB LDS-DMA loads per wave per chunk
-  constexpr int FM = MT / 16, FN = 2, KSC = kStreamKC / 32, KS = KSC * KC;
-  constexpr int Q = MT / 16;                     // 16-byte stores per wave per tile (MT/4 rows)
+  constexpr int P = SLOT / 1024 / NW;            // 1 KiB LDS-DMA loads per wave per chunk
+  constexpr int FM = RW / 16, FN = 2, KSC = kStreamKC / 32, KS = KSC * KC;
+  constexpr int Q = RW / 16;                     // 16-byte stores per wave per tile (MT/NW = RW/4 rows)
   constexpr int QC = Q / KC;                     // ... per chunk
   constexpr int STG = MT * 256;                  // one tile's results, two buffers
   constexpr int SLOTS = MT == 64 ? 4 : 3;        // ring depth (chunks)
@@ -67,6 +73,7 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, wc = wave & 3;  // row group, column slice
   const int r16 = lane & 15, G = lane >> 4;
   const int M = p.M, N = p.N, K = p.K;
   const int tiles_n = p.tiles_n;
@@ -74,13 +81,13 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
   const int ntiles = total_tiles > me ? (total_tiles - me + step - 1) / step : 0;
   const int nchunks = ntiles * KC;
 
-  // ---- A fragments (rows 16i + r16, k = 32s + 8G .. +7), zero past M and K ----
+  // ---- A fragments (rows RW grp + 16i + r16, k = 32s + 8G .. +7), zero past M and K ----
   u32x4 fa[FM][KS];
   {
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A);
     static_for<FM * KS>([&](auto xc) {
       constexpr int x = decltype(xc)::value, i = x / KS, s = x % KS;
-      const int m = 16 * i + r16, k = 32 * s + 8 * G;
+      const int m = RW * grp + 16 * i + r16, k = 32 * s + 8 * G;
       fa[i][s] = buf_load16(ra, (m < M && k < K) ? (uint32_t)(m * p.lda + k) * 2u : kBufOOB);
     });
   }
@@ -88,7 +95,7 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
   if constexpr (BIAS == 2) {
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.bias), 0, 2 * M, kBufWord3);
 #pragma unroll
-    for (int i = 0; i < FM; ++i) bias_m[i] = from_bits<T>(buf_load2(rb, (uint32_t)(2 * (16 * i + r16))));
+    for (int i = 0; i < FM; ++i) bias_m[i] = from_bits<T>(buf_load2(rb, (uint32_t)(2 * (RW * grp + 16 * i + r16))));
   }
   // Make these values definitions of an asm statement placed after a full wait: the
   // compiler counts only its own vector-memory instructions, so a wait it derived for
@@ -138,16 +145,16 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
   uint32_t fb_off[FN];
   const int kr = 8 * G + (r16 >> 2);
 #pragma unroll
-  for (int j = 0; j < FN; ++j) fb_off[j] = kn_off(kr, PITCH, (32 * wave + 16 * j + 4 * (r16 & 3)) * 2);
+  for (int j = 0; j < FN; ++j) fb_off[j] = kn_off(kr, PITCH, (32 * wc + 16 * j + 4 * (r16 & 3)) * 2);
 
-  // ---- results: after one permlane16 swap per dword, lane (r16, G) holds row 16i + r16,
+  // ---- results: after one permlane16 swap per dword, lane (r16, G) holds row RW grp + 16i + r16,
   // columns col .. col+7 of the tile; they go to staging buffer i % 2 as 16-byte chunk
   // col/8 of the row, at chunk position (col/8) ^ (row % 16) (conflict-free writes and
   // row reads) ----
-  const int col = 32 * wave + 16 * (G & 1) + 8 * (G >> 1);
+  const int col = 32 * wc + 16 * (G & 1) + 8 * (G >> 1);
   unsigned char* const stg0 = smem + SLOTS * SLOT;
   // Part `part` of KC of this wave's stores of tile i: QC stores of 4 x 256-byte rows
-  // (rows MT/4 wave + 4 QC part .. of the wave's MT/4 rows; an empty descriptor when there
+  // (rows RW/4 wave + 4 QC part .. of the wave's RW/4 rows; an empty descriptor when there
   // is no tile i): always QC instructions.
   auto store = [&](int i, auto partc) {
     constexpr int part = decltype(partc)::value;
@@ -162,12 +169,12 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
     u32x4 v[QC];
 #pragma unroll
     for (int q = 0; q < QC; ++q) {
-      const int row = (MT / 4) * wave + 4 * (QC * part + q) + (lane >> 4);
+      const int row = (RW / 4) * wave + 4 * (QC * part + q) + (lane >> 4);
       v[q] = *(const u32x4*)(stg + row * 256 + ((ch ^ (row & 15)) << 4));
     }
 #pragma unroll
     for (int q = 0; q < QC; ++q) {
-      const int row = (MT / 4) * wave + 4 * (QC * part + q) + (lane >> 4);
+      const int row = (RW / 4) * wave + 4 * (QC * part + q) + (lane >> 4);
       const uint32_t off = (col_ok && row < M) ? (uint32_t)(row * p.ldc + 8 * ch) * 2u : kBufOOB;
       __builtin_amdgcn_raw_buffer_store_b128(v[q], rc, off, 0, kStreamStorePolicy);
     }
@@ -201,24 +208,27 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
       issue(c + SLOTS - 1, std::integral_constant<int, (h + SLOTS - 1) % KC>{});
 
       const unsigned char* sb = smem + (c % SLOTS) * SLOT;
-      u32x4 fb[KSC][FN];
-      static_for<KSC * FN * 2>([&](auto rc) {
-        constexpr int r = decltype(rc)::value, s = r / (2 * FN), j = (r / 2) % FN, half = r % 2;
-        typedef short s16x4 __attribute__((ext_vector_type(4)));
-        const unsigned char* q = sb + fb_off[j] + (32 * s + 4 * half) * PITCH;
-        const u32x2 v = __builtin_bit_cast(
-            u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q));
-        if constexpr (half == 0) {
-          fb[s][j].x = v.x;
-          fb[s][j].y = v.y;
-        } else {
-          fb[s][j].z = v.x;
-          fb[s][j].w = v.y;
-        }
-      });
-      static_for<KSC * FM * FN>([&](auto xc) {
-        constexpr int x = decltype(xc)::value, s = x / (FM * FN), ii = (x / FN) % FM, j = x % FN;
-        acc[ii][j] = Mfma<T>::mma(fb[s][j], fa[ii][KSC * h + s], acc[ii][j]);
+      static_for<KSC>([&](auto sc) {  // sub-steps of 32 k: B fragments, then their MFMAs
+        constexpr int s = decltype(sc)::value;
+        u32x4 fb[FN];
+        static_for<FN * 2>([&](auto rc) {
+          constexpr int r = decltype(rc)::value, j = r / 2, half = r % 2;
+          typedef short s16x4 __attribute__((ext_vector_type(4)));
+          const unsigned char* q = sb + fb_off[j] + (32 * s + 4 * half) * PITCH;
+          const u32x2 v = __builtin_bit_cast(
+              u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q));
+          if constexpr (half == 0) {
+            fb[j].x = v.x;
+            fb[j].y = v.y;
+          } else {
+            fb[j].z = v.x;
+            fb[j].w = v.y;
+          }
+        });
+        static_for<FM * FN>([&](auto xc) {
+          constexpr int x = decltype(xc)::value, ii = x / FN, j = x % FN;
+          acc[ii][j] = Mfma<T>::mma(fb[j], fa[ii][KSC * h + s], acc[ii][j]);
+        });
       });
     });
     // results -> staging buffer i % 2, last read by the stores of tile i-2 (during the
@@ -242,7 +252,7 @@ __global__ void __launch_bounds__(256, 1) gemm_stream_kernel(const GemmParams p,
         P0[w] = sw[0];
         P1[w] = sw[1];
       }
-      const int row = 16 * ii + r16;
+      const int row = RW * grp + 16 * ii + r16;
       *(u32x4*)(stg + row * 256 + (((col >> 3) ^ (row & 15)) << 4)) = u32x4{P0[0], P0[1], P1[0], P1[1]};
     }
   }

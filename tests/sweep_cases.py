@@ -67,7 +67,7 @@ def draw_stream_case(rng: np.random.Generator, idx: int, wide_rows: bool) -> dic
     (M of 65 to 128 if wide_rows)."""
     dtype = ["fp16", "bf16"][rng.integers(2)]
     M = int(rng.integers(65, 129)) if wide_rows else int(rng.integers(1, 65))
-    K = int(rng.choice([8, 64, 72, 128] if M > 64 else [8, 64, 128, 136, 200, 256]))
+    K = int(rng.choice([8, 64, 72, 128, 136, 200, 256]))
     N = int(rng.choice([8192, 8200, 16384, 16376]))
     batch = -(-4096 // -(-N // 128))
     ldb = N + int(rng.choice([0, 8]))

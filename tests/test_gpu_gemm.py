@@ -742,6 +742,9 @@ def test_tiled_split_k_batched(dtype):
     (64, 16384, 256, 32, True),   # K = 256: two chunks of 128 k per tile
     (48, 8200, 200, 64, False),   # second chunk ragged (72 k), M and N ragged
     (8, 131072, 136, 4, True),    # second chunk of 8 k
+    (128, 16384, 256, 32, True),  # 128 rows in two groups of 4 waves, K = 256
+    (96, 8200, 200, 64, False),   # ... M, N and the second chunk ragged
+    (72, 131072, 136, 4, True),   # ... second chunk of 8 k
 ])
 def test_stream_kernel(dtype, M, N, K, batch, bias):
     """Short-K products over many columns with one A for the whole batch (the 1x1

@@ -71,15 +71,16 @@ def test_stream_kernel_for_convolution_shapes():
     assert _prepared_kernel(cabi.BF16, 40, 16384, 72, 32, 0)[0] == K_STREAM      # 4096 tiles, ragged M, K
     assert _prepared_kernel(cabi.F16, 1, 524288, 8, 1, 0)[0] == K_STREAM
     assert _prepared_kernel(cabi.F16, 64, 8200, 128, 64, 0)[0] == K_STREAM       # 65 tiles per image
-    # up to 64 rows, K up to 256 (two chunks of 128 k per tile)
+    # K up to 256 (two chunks of 128 k per tile), up to 64 rows or 65..128
     assert _prepared_kernel(cabi.F16, 64, 16384, 136, 64, 0)[0] == K_STREAM
     assert _prepared_kernel(cabi.BF16, 64, 16384, 256, 32, 0, cabi.BIAS_PER_ROW, bias=0x1000)[0] == K_STREAM
-    # not the streaming kernel: too few tiles per CU, K above 256 (above 128 for 65..128
-    # rows), M above 128, one A per batch entry, a bias per column, a misaligned A, or rows
-    # of C not 16-byte multiples
+    assert _prepared_kernel(cabi.F16, 65, 16384, 136, 64, 0)[0] == K_STREAM128
+    assert _prepared_kernel(cabi.BF16, 128, 16384, 256, 32, 0, cabi.BIAS_PER_ROW, bias=0x1000)[0] == K_STREAM128
+    # not the streaming kernel: too few tiles per CU, K above 256, M above 128, one A per
+    # batch entry, a bias per column, a misaligned A, or rows of C not 16-byte multiples
     assert _prepared_kernel(cabi.F16, 64, 16384, 128, 31, 0)[0] != K_STREAM
     assert _prepared_kernel(cabi.F16, 64, 16384, 264, 64, 0)[0] != K_STREAM
-    assert _prepared_kernel(cabi.F16, 65, 16384, 136, 64, 0)[0] not in (K_STREAM, K_STREAM128)
+    assert _prepared_kernel(cabi.F16, 128, 16384, 264, 64, 0)[0] not in (K_STREAM, K_STREAM128)
     kid, desc = _prepared_kernel(cabi.F16, 65, 16384, 128, 64, 0)
     assert kid == K_STREAM128 and "tile=128x128" in desc, desc   # 65..128 rows: 128-row tiles
     assert _prepared_kernel(cabi.BF16, 128, 16384, 128, 64, 0, cabi.BIAS_PER_ROW, bias=0x1000)[0] == K_STREAM128
