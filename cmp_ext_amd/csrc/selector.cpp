@@ -222,7 +222,7 @@ int make_plan_core(const Request& r, Plan* plan) {
         p.kernel = kSkinny;
         p.bn = 32;
       }
-    } else if (fast && r.layout == kKN && r.M <= 128 && r.K <= 256 && r.N % 8 == 0 && r.ldc % 8 == 0 &&
+    } else if (fast && r.layout == kKN && r.M <= kStreamMaxRows && r.K <= 256 && r.N % 8 == 0 && r.ldc % 8 == 0 &&
                (!batched || (r.stride_a == 0 && r.stride_c % 8 == 0)) && (!r.has_bias || r.bias_row) &&
                128 * r.ldb * 2 <= kIntMax && 128 * r.ldc * 2 <= kIntMax &&
                cdiv(r.N, 128) * r.batch >= 16 * kNumCUs && cdiv(r.N, 128) * r.batch <= kIntMax) {
@@ -280,7 +280,10 @@ int make_plan_core(const Request& r, Plan* plan) {
     }
   }
   if (p.splits == 0) p.splits = 1;
-  if (p.kernel == kSkinny || p.kernel == kSkinnyWide || p.kernel == kSkinnyNK) {
+  if (p.kernel == kSkinny || p.kernel == kSkinnyWide || p.kernel == kSkinnyNK || p.kernel == kStream64x128 ||
+      p.kernel == kStream128x128) {
+    // one grid column per column strip or tile: these kernels cover all of M themselves (the
+    // streaming kernel in row blocks of bm)
     p.tiles_m = 1;
     p.tiles_n = (int)cdiv(r.N, p.bn) * (p.kernel == kSkinnyWide ? p.splits : 1);
   } else {

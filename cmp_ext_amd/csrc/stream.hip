@@ -1,5 +1,5 @@
-// Launcher of the short-K streaming kernel (f16/bf16, M <= 128, K <= 256, bias none or per
-// row).
+// Launcher of the short-K streaming kernel (f16/bf16, M <= 512 in row blocks of 64 or 128,
+// K <= 256, bias none or per row).
 #include "kernels.h"
 #include "selector.h"
 #include "stream_kernel.h"
@@ -11,7 +11,9 @@ namespace cmpext3 {
 // channels 134.5 / 129.4, 64 <- 160 91.6 / 86.8, 48 <- 200 102.0 / 98.2; but 64 <- 136
 // 71.3 / 76.2, and with one chunk (K <= 128) it is always slower: 64 <- 128 62.7 / 75.4,
 // 16 <- 128 51.7 / 57.8, 32 <- 64 37.5 / 38.0.
-static bool stream_nt(const GemmParams& p) { return p.K >= 160; }
+// With several row blocks the later blocks read each B chunk from L2, which the
+// non-temporal policy would give up: only for M <= 128.
+static bool stream_nt(const GemmParams& p) { return p.K >= 160 && p.M <= 128; }
 
 template <typename T, int WG, int KC, bool NT>
 static void launch_stream_t(const GemmParams& p, int total, unsigned wgs, hipStream_t s) {
@@ -43,13 +45,22 @@ static void launch_stream_shape(const GemmParams& p, int total, unsigned wgs, hi
 }
 
 hipError_t launch_stream(DType dt, const GemmParams& p, dim3 grid, hipStream_t s) {
-  // grid.x = 128-column tiles of one product, grid.z = batch entries: one persistent
-  // workgroup per CU walks all of them
+  // grid.x = 128-column tiles of one product (all of M: the kernel covers the rows itself),
+  // grid.z = batch entries: persistent workgroups, a set per row block of 64 (M <= 64) or 128
+  // rows, walk all of them.  A grid that does not match N would send the walk past the
+  // operands, so it is an error.
+  if (grid.y != 1 || (int64_t)grid.x != ((int64_t)p.N + kStreamN - 1) / kStreamN || (int)grid.x != p.tiles_n)
+    return hipErrorInvalidValue;
   const int64_t total = (int64_t)grid.x * grid.z;
   if (total <= 0) return hipSuccess;
-  if (total > 0x7FFFFFFF || (p.bias != nullptr && !p.bias_row) || p.M > 128 || p.K > 2 * kStreamKC)
+  if (total > 0x7FFFFFFF || (p.bias != nullptr && !p.bias_row) || p.M > kStreamMaxRows || p.K > 2 * kStreamKC)
     return hipErrorInvalidValue;
-  const unsigned wgs = (unsigned)std::min<int64_t>(total, kNumCUs);
+  const int mt = p.M > 64 ? 128 : 64;
+  const int row_blocks = (p.M + mt - 1) / mt;
+  // workgroups per row block: a multiple of 8 (one per XCD and round) when there are 8 or more
+  int64_t per_block = std::min<int64_t>(total, kNumCUs / row_blocks);
+  if (per_block >= 8) per_block -= per_block % 8;
+  const unsigned wgs = (unsigned)(per_block * row_blocks);
   if (dt == kF16)
     launch_stream_shape<_Float16>(p, (int)total, wgs, s);
   else

@@ -1,5 +1,5 @@
 // Short-K f16/bf16 GEMM over many columns: C[b] = A * B[b] (+ bias per row),
-// M <= 128 and K <= 256, B as [K,N] -- the shape of a 1x1 convolution over NCHW
+// M <= 512 and K <= 256, B as [K,N] -- the shape of a 1x1 convolution over NCHW
 // activations (A = the weight, shared by every batch entry; B[b] = one image's
 // [C_in][H*W]; C[b] = its [C_out][H*W]); counterpart of the reference's conv2d
 // routed through its GEMM (csrc/main.cpp:402-424).
@@ -8,8 +8,10 @@
 // C out, and a tile kernel that holds one 64 x 256 tile per workgroup leaves
 // each CU idle between its tiles' loads (measured 3.9 TB/s).  Here a persistent
 // workgroup per CU walks the 128-column tiles t = blockIdx.x, + gridDim.x, ...
-// (batch entry t / tiles_n) with
-//   * tiles of MT = 64 WG rows (all of M) by 128 columns, WG = 1 or 2 groups of 4 waves,
+// (batch entry t / tiles_n) of its row block with
+//   * tiles of MT = 64 WG rows by 128 columns (M > 128: row blocks of 128 rows, each with
+//     its own set of workgroups, the sets in step so that a B chunk comes from HBM once
+//     and from L2 for the other blocks), WG = 1 or 2 groups of 4 waves,
 //     group g computing rows 64 g .. 64 g + 63; each tile read as KC = 1 or 2 chunks of
 //     128 k-rows (K <= 128 KC);
 //   * A held in registers for the whole kernel (each wave its 64 rows x 128 KC as MFMA
@@ -75,16 +77,24 @@ __global__ void __launch_bounds__(256 * WG, 1) gemm_stream_kernel(const GemmPara
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = wave >> 2, wc = wave & 3;  // row group, column slice
   const int r16 = lane & 15, G = lane >> 4;
-  const int M = p.M, N = p.N, K = p.K;
+  const int N = p.N, K = p.K;
   const int tiles_n = p.tiles_n;
-  const int me = blockIdx.x, step = gridDim.x;
+  // Row blocks of MT rows: gridDim.x / row_blocks workgroups per block, each walking the
+  // column tiles of its block.  The launcher makes that count a multiple of 8, so workgroup
+  // j of every block runs on the same XCD (workgroups go to the XCDs round robin) and, the
+  // blocks walking their tiles in step, the later blocks find each B chunk in that L2.
+  const int row_blocks = (p.M + MT - 1) / MT;
+  const int step = gridDim.x / row_blocks;
+  const int rblk = blockIdx.x / step, me = blockIdx.x - rblk * step;
+  const int m_base = rblk * MT;
+  const int M = min(p.M - m_base, MT);  // rows of this block
   const int ntiles = total_tiles > me ? (total_tiles - me + step - 1) / step : 0;
   const int nchunks = ntiles * KC;
 
   // ---- A fragments (rows RW grp + 16i + r16, k = 32s + 8G .. +7), zero past M and K ----
   u32x4 fa[FM][KS];
   {
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc((const T*)p.A + (int64_t)m_base * p.lda);
     static_for<FM * KS>([&](auto xc) {
       constexpr int x = decltype(xc)::value, i = x / KS, s = x % KS;
       const int m = RW * grp + 16 * i + r16, k = 32 * s + 8 * G;
@@ -93,7 +103,8 @@ __global__ void __launch_bounds__(256 * WG, 1) gemm_stream_kernel(const GemmPara
   }
   float bias_m[FM] = {};
   if constexpr (BIAS == 2) {
-    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.bias), 0, 2 * M, kBufWord3);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((T*)const_cast<void*>(p.bias) + m_base, 0, 2 * M, kBufWord3);
 #pragma unroll
     for (int i = 0; i < FM; ++i) bias_m[i] = from_bits<T>(buf_load2(rb, (uint32_t)(2 * (RW * grp + 16 * i + r16))));
   }
@@ -161,7 +172,7 @@ __global__ void __launch_bounds__(256 * WG, 1) gemm_stream_kernel(const GemmPara
     const bool live = i >= 0 && i < ntiles;
     const int t = live ? me + i * step : 0;
     const int bz = t / tiles_n, n0 = (t - bz * tiles_n) * kStreamN;
-    T* cb = (T*)p.C + (int64_t)bz * p.stride_c + n0;
+    T* cb = (T*)p.C + (int64_t)bz * p.stride_c + (int64_t)m_base * p.ldc + n0;
     const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(cb, 0, live ? (int)kBufRecords : 0, kBufWord3);
     const unsigned char* stg = stg0 + (i & 1) * STG;
     const int ch = lane & 15;

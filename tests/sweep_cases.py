@@ -64,9 +64,9 @@ def draw_case(rng: np.random.Generator, idx: int) -> dict:
 
 def draw_stream_case(rng: np.random.Generator, idx: int, wide_rows: bool) -> dict:
     """A 1x1-convolution-shaped case: one A for the batch, B as [K,N], >= 4096 column tiles
-    (M of 65 to 128 if wide_rows)."""
+    (M of 65 to 320 if wide_rows)."""
     dtype = ["fp16", "bf16"][rng.integers(2)]
-    M = int(rng.integers(65, 129)) if wide_rows else int(rng.integers(1, 65))
+    M = int(rng.integers(65, 321)) if wide_rows else int(rng.integers(1, 65))
     K = int(rng.choice([8, 64, 72, 128, 136, 200, 256]))
     N = int(rng.choice([8192, 8200, 16384, 16376]))
     batch = -(-4096 // -(-N // 128))

@@ -52,7 +52,8 @@ SHAPES = [(2, 256, 32, 32, 512), (2, 512, 64, 64, 16), (1, 64, 7, 7, 96), (3, 40
           (8, 64, 256, 256, 48),  # 4096 column tiles of 128 pixels: the streaming kernel
           (8, 96, 256, 256, 128),  # ... with 128-row tiles
           (16, 200, 128, 256, 56),  # ... K = 200 in two chunks of 128 input channels
-          (16, 192, 128, 256, 96)]  # ... 128-row tiles in two groups of 4 waves
+          (16, 192, 128, 256, 96),  # ... 128-row tiles in two groups of 4 waves
+          (16, 96, 128, 256, 320)]  # ... three row blocks of 128 output channels
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])

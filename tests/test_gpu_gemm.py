@@ -745,6 +745,9 @@ def test_tiled_split_k_batched(dtype):
     (128, 16384, 256, 32, True),  # 128 rows in two groups of 4 waves, K = 256
     (96, 8200, 200, 64, False),   # ... M, N and the second chunk ragged
     (72, 131072, 136, 4, True),   # ... second chunk of 8 k
+    (256, 16384, 64, 32, True),   # two row blocks of 128
+    (200, 8200, 136, 64, False),  # ... the second of 72 rows, N and K ragged
+    (512, 16384, 256, 32, True),  # four row blocks, K = 256
 ])
 def test_stream_kernel(dtype, M, N, K, batch, bias):
     """Short-K products over many columns with one A for the whole batch (the 1x1
