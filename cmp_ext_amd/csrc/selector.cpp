@@ -225,16 +225,19 @@ int make_plan_core(const Request& r, Plan* plan) {
     } else if (fast && r.layout == kKN && r.M <= kStreamMaxRows && r.K <= 256 && r.N % 8 == 0 && r.ldc % 8 == 0 &&
                (!batched || (r.stride_a == 0 && r.stride_c % 8 == 0)) && (!r.has_bias || r.bias_row) &&
                128 * r.ldb * 2 <= kIntMax && 128 * r.ldc * 2 <= kIntMax &&
-               cdiv(r.N, 128) * r.batch >= 16 * kNumCUs && cdiv(r.N, 128) * r.batch <= kIntMax) {
+               cdiv(r.N, 128) * r.batch * cdiv(r.M, r.M <= 64 ? 64 : 128) >= 16 * kNumCUs &&
+               cdiv(r.N, 128) * r.batch <= kIntMax) {
       // Short K over many columns with one A (a 1x1 convolution: weight x every image's
       // pixels): bound by streaming B in and C out, which persistent workgroups with
       // three tiles in flight do faster than one tile per workgroup once each has >= 16
       // tiles (MI355X, vs the 64x256 tile: 64 x 16384 x 128 x 64 images 64.0 vs 106.8
       // us, 64 x 1048576 x 128 60.5 vs 100.2, 64 x 16384 x 64 x 32 images 23.4 vs 38.2;
       // with 2 .. 8 tiles each it is up to 10 % slower).
+      // (>= 16 tiles per workgroup: row blocks x column tiles over the 256 workgroups)
       p.kernel = r.M <= 64 ? kStream64x128 : kStream128x128;
       p.bm = r.M <= 64 ? 64 : 128;
       p.bn = 128;
+      p.threads = r.M <= 64 ? 256 : 512;
     } else if (fast && r.M <= 64 && r.K <= 1024 && cdiv(r.N, 256) * r.batch >= kNumCUs) {
       // Short-K products with few rows and many columns are HBM-bound; 64-row tiles
       // waste no MFMA rows and keep more loads in flight per CU (MI355X, 64x256 vs

@@ -53,7 +53,7 @@ std::string describe(const Request& r, const Plan& p);
 
 // Number of compute units the tile cost model assumes (MI355X: 256).
 constexpr int kNumCUs = 256;
-// Most rows of C the streaming kernel takes (four row blocks of 128).
-constexpr int kStreamMaxRows = 512;
+// Most rows of C the streaming kernel takes (16 row blocks of 128).
+constexpr int kStreamMaxRows = 2048;
 
 }  // namespace cmpext3

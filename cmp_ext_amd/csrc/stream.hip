@@ -1,4 +1,4 @@
-// Launcher of the short-K streaming kernel (f16/bf16, M <= 512 in row blocks of 64 or 128,
+// Launcher of the short-K streaming kernel (f16/bf16, M <= 2048 in row blocks of 64 or 128,
 // K <= 256, bias none or per row).
 #include "kernels.h"
 #include "selector.h"

@@ -1,5 +1,5 @@
 // Short-K f16/bf16 GEMM over many columns: C[b] = A * B[b] (+ bias per row),
-// M <= 512 and K <= 256, B as [K,N] -- the shape of a 1x1 convolution over NCHW
+// M <= 2048 and K <= 256, B as [K,N] -- the shape of a 1x1 convolution over NCHW
 // activations (A = the weight, shared by every batch entry; B[b] = one image's
 // [C_in][H*W]; C[b] = its [C_out][H*W]); counterpart of the reference's conv2d
 // routed through its GEMM (csrc/main.cpp:402-424).
@@ -9,9 +9,9 @@
 // each CU idle between its tiles' loads (measured 3.9 TB/s).  Here a persistent
 // workgroup per CU walks the 128-column tiles t = blockIdx.x, + gridDim.x, ...
 // (batch entry t / tiles_n) of its row block with
-//   * tiles of MT = 64 WG rows by 128 columns (M > 128: row blocks of 128 rows, each with
-//     its own set of workgroups, the sets in step so that a B chunk comes from HBM once
-//     and from L2 for the other blocks), WG = 1 or 2 groups of 4 waves,
+//   * tiles of MT = 64 WG rows by 128 columns (M > 128: up to 16 row blocks of 128 rows,
+//     each with its own set of workgroups, the sets in step so that a B chunk comes from
+//     HBM once and from L2 for the other blocks), WG = 1 or 2 groups of 4 waves,
 //     group g computing rows 64 g .. 64 g + 63; each tile read as KC = 1 or 2 chunks of
 //     128 k-rows (K <= 128 KC);
 //   * A held in registers for the whole kernel (each wave its 64 rows x 128 KC as MFMA

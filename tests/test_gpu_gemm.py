@@ -748,6 +748,7 @@ def test_tiled_split_k_batched(dtype):
     (256, 16384, 64, 32, True),   # two row blocks of 128
     (200, 8200, 136, 64, False),  # ... the second of 72 rows, N and K ragged
     (512, 16384, 256, 32, True),  # four row blocks, K = 256
+    (1000, 16384, 128, 16, True),  # eight row blocks, the last of 104 rows
 ])
 def test_stream_kernel(dtype, M, N, K, batch, bias):
     """Short-K products over many columns with one A for the whole batch (the 1x1

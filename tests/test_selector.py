@@ -76,7 +76,7 @@ def test_stream_kernel_for_convolution_shapes():
     assert _prepared_kernel(cabi.BF16, 64, 16384, 256, 32, 0, cabi.BIAS_PER_ROW, bias=0x1000)[0] == K_STREAM
     assert _prepared_kernel(cabi.F16, 65, 16384, 136, 64, 0)[0] == K_STREAM128
     assert _prepared_kernel(cabi.BF16, 128, 16384, 256, 32, 0, cabi.BIAS_PER_ROW, bias=0x1000)[0] == K_STREAM128
-    # not the streaming kernel: too few tiles per CU, K above 256, M above 512, one A per
+    # not the streaming kernel: too few tiles per CU, K above 256, M above 2048, one A per
     # batch entry, a bias per column, a misaligned A, or rows of C not 16-byte multiples
     assert _prepared_kernel(cabi.F16, 64, 16384, 128, 31, 0)[0] != K_STREAM
     assert _prepared_kernel(cabi.F16, 64, 16384, 264, 64, 0)[0] != K_STREAM
@@ -84,13 +84,18 @@ def test_stream_kernel_for_convolution_shapes():
     kid, desc = _prepared_kernel(cabi.F16, 65, 16384, 128, 64, 0)
     assert kid == K_STREAM128 and "tile=128x128" in desc, desc   # 65..128 rows: 128-row tiles
     assert _prepared_kernel(cabi.BF16, 128, 16384, 128, 64, 0, cabi.BIAS_PER_ROW, bias=0x1000)[0] == K_STREAM128
-    # more than 128 rows: row blocks of 128, up to 512 rows; the grid counts column tiles
+    # more than 128 rows: row blocks of 128, up to 2048 rows; the grid counts column tiles
     # only (the kernel walks its row blocks itself): 128 tiles x 1 x 32 images
     assert _prepared_kernel(cabi.F16, 129, 16384, 128, 64, 0)[0] == K_STREAM128
     kid, desc = _prepared_kernel(cabi.F16, 256, 16384, 64, 32, 0)
-    assert kid == K_STREAM128 and "grid=1x128x32 " in desc, desc
+    assert kid == K_STREAM128 and "grid=1x128x32 " in desc and "threads=512" in desc, desc
     assert _prepared_kernel(cabi.BF16, 512, 16384, 256, 32, 0, cabi.BIAS_PER_ROW, bias=0x1000)[0] == K_STREAM128
-    assert _prepared_kernel(cabi.F16, 513, 16384, 128, 64, 0)[0] not in (K_STREAM, K_STREAM128)
+    assert _prepared_kernel(cabi.F16, 2048, 16384, 128, 8, 0)[0] == K_STREAM128
+    assert _prepared_kernel(cabi.F16, 2049, 16384, 128, 8, 0)[0] not in (K_STREAM, K_STREAM128)
+    # >= 16 tiles per workgroup counts the row blocks: 1024 rows x 2048 column tiles (8 x 2048
+    # = 16384 block-tiles), but not 128 rows x 2048 column tiles
+    assert _prepared_kernel(cabi.F16, 1024, 16384, 256, 16, 0)[0] == K_STREAM128
+    assert _prepared_kernel(cabi.F16, 128, 16384, 256, 16, 0)[0] != K_STREAM128
     assert _prepared_kernel(cabi.F16, 64, 16384, 128, 64, 64 * 128)[0] != K_STREAM
     assert _prepared_kernel(cabi.F16, 64, 16384, 128, 64, 0, 0, bias=0x1000)[0] != K_STREAM
     assert _prepared_kernel(cabi.F16, 64, 16384, 128, 64, 0, align=8)[0] != K_STREAM
