@@ -341,8 +341,8 @@ def caller_inputs(c, device: str, seed: int = 0):
         return draw((M, K), 1.0), draw((N, K), K ** -0.5), draw((N,), 0.1)
     if c["op"] == "bmm":
         return draw((Bn, M, K), 1.0), draw((Bn, K, N), K ** -0.5)
-    hw = int(round(N ** 0.5))
-    return draw((Bn, K, hw, hw), 1.0), draw((M, K, 1, 1), K ** -0.5), draw((M,), 0.1)
+    h = c.get("H", int(round(N ** 0.5)))
+    return draw((Bn, K, h, N // h), 1.0), draw((M, K, 1, 1), K ** -0.5), draw((M,), 0.1)
 
 
 def caller_fn(c, cm):
@@ -591,6 +591,10 @@ def main() -> int:
                          "board power and shader clock (0: skip)")
     ap.add_argument("--caller", default=None, choices=sorted(CALLERS),
                     help="time only this caller and print its JSON object (for profiling)")
+    ap.add_argument("--conv-shape", default=None, metavar="B,CIN,H,W,COUT",
+                    help="time cmpext3.conv2d 1x1 (with bias) on this shape instead and print its JSON "
+                         "object, as --caller does (for profiling the streaming kernel on other shapes)")
+    ap.add_argument("--conv-dtype", default="fp16", choices=["fp16", "bf16", "fp32"])
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of GEMMs, run a plain device copy of MIB MiB per step (reference "
                          "point for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
@@ -615,6 +619,15 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes_per_step": n * 4, "steps": args.warmup + args.steps}))
         return 0
+    if args.conv_shape:
+        try:
+            Bn, cin, h, w, cout = (int(x) for x in args.conv_shape.split(","))
+        except ValueError:
+            raise SystemExit("bench.py: --conv-shape takes B,CIN,H,W,COUT (integers)")
+        name = f"conv1x1_{args.conv_dtype}_{Bn}x{cin}x{h}x{w}_to{cout}"
+        CALLERS[name] = dict(op="conv", dtype=args.conv_dtype, M=cout, N=h * w, K=cin, batch=Bn, H=h, hbm=True,
+                             desc=f"cmpext3.conv2d 1x1 with bias: input [{Bn},{cin},{h},{w}] -> {cout} channels")
+        args.caller = name
     if args.caller:
         log(f"timing {args.caller} ({args.warmup} warm-up + {args.steps} steps)")
         r = time_caller(args.caller, args.steps, args.warmup, not args.no_torch)
