@@ -17,13 +17,13 @@
 //   * A held in registers for the whole kernel (each wave its 64 rows x 128 KC as MFMA
 //     fragments);
 //   * B chunks ([128][128] = 32 KiB, rows of 256 bytes) streamed global -> LDS by
-//     LDS-DMA through a ring of four slots (three for MT = 128, whose results
-//     need twice the staging), three (two) chunks in flight;
+//     LDS-DMA through a ring of four slots, three chunks in flight;
 //   * per chunk and wave (its rows x 32 columns; the 4 waves of a group split the
 //     128 columns) 4 sub-steps of 32 k on 16x16x32 MFMAs, B fragments by
 //     ds_read_b64_tr_b16 as in the tile kernel's [K,N] path;
 //   * the tile's results staged in LDS (row-major, 16-byte chunks XOR-swizzled by
-//     row) and written during the next tile's chunks, after their barriers: each
+//     row; two buffers for MT = 64, one for MT = 128) and written during the next
+//     tile's chunks, after their barriers: each
 //     wave stores MT/waves whole rows of 256 bytes with non-temporal 16-byte stores
 //     (full cache lines that go straight to HBM instead of waiting in L2 as dirty
 //     lines; measured on MI355X for the 64 x 16384 x 128 x 64 convolution: 62.4
@@ -65,12 +65,16 @@ __global__ void __launch_bounds__(256 * WG, 1) gemm_stream_kernel(const GemmPara
   constexpr int FM = RW / 16, FN = 2, KSC = kStreamKC / 32, KS = KSC * KC;
   constexpr int Q = RW / 16;                     // 16-byte stores per wave per tile (MT/NW = RW/4 rows)
   constexpr int QC = Q / KC;                     // ... per chunk
-  constexpr int STG = MT * 256;                  // one tile's results, two buffers
-  constexpr int SLOTS = MT == 64 ? 4 : 3;        // ring depth (chunks)
+  constexpr int STG = MT * 256;                  // one tile's results
+  // Staging buffers: two for MT = 64 (a tile's results go to one while the other's are
+  // stored); one for MT = 128, with a barrier before it is overwritten, so that the ring
+  // keeps four slots (three chunks in flight) there too.
+  constexpr int SB = MT == 64 ? 2 : 1;
+  constexpr int SLOTS = 4;                       // ring depth (chunks)
   static_assert(Q % KC == 0, "stores spread evenly over the chunks");
   static_assert((SLOTS - 2) * (P + QC) <= 63, "vmcnt range");
-  static_assert(SLOTS * SLOT + 2 * STG <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[SLOTS * SLOT + 2 * STG];
+  static_assert(SLOTS * SLOT + SB * STG <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[SLOTS * SLOT + SB * STG];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -174,7 +178,7 @@ __global__ void __launch_bounds__(256 * WG, 1) gemm_stream_kernel(const GemmPara
     const int bz = t / tiles_n, n0 = (t - bz * tiles_n) * kStreamN;
     T* cb = (T*)p.C + (int64_t)bz * p.stride_c + (int64_t)m_base * p.ldc + n0;
     const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(cb, 0, live ? (int)kBufRecords : 0, kBufWord3);
-    const unsigned char* stg = stg0 + (i & 1) * STG;
+    const unsigned char* stg = stg0 + (SB == 2 ? (i & 1) * STG : 0);
     const int ch = lane & 15;
     const bool col_ok = n0 + 8 * ch < N;
     u32x4 v[QC];
@@ -242,9 +246,12 @@ __global__ void __launch_bounds__(256 * WG, 1) gemm_stream_kernel(const GemmPara
         });
       });
     });
-    // results -> staging buffer i % 2, last read by the stores of tile i-2 (during the
-    // chunks of tile i-1), which every wave finished before this tile's barriers
-    unsigned char* stg = stg0 + (i & 1) * STG;
+    // results -> staging: with two buffers, buffer i % 2, last read by the stores of tile
+    // i-2 (during the chunks of tile i-1), which every wave finished before this tile's
+    // barriers; with one, the buffer the stores of tile i-1 read during this tile's chunks,
+    // so every wave first waits for the others to be past those reads
+    if constexpr (SB == 1) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
+    unsigned char* stg = stg0 + (SB == 2 ? (i & 1) * STG : 0);
 #pragma unroll
     for (int ii = 0; ii < FM; ++ii) {
       f32x4 v0 = acc[ii][0], v1 = acc[ii][1];
