@@ -6,6 +6,8 @@
 #include "selector.h"
 
 #include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include <algorithm>
 
@@ -119,6 +121,114 @@ const char* kernel_name(KernelId id) {
 }  // namespace
 
 namespace {
+// Tuning override: CMPEXT3_GEMM_CONFIG="kernel=<name>[,splits=<s>]" (names as in the plan
+// strings, e.g. tile128x128, stream64x128, generic64x64, f32tile96x64) replaces the
+// selector's choice wherever that kernel's own requirements hold for the call; otherwise,
+// and for an unknown name or malformed value, it is ignored.  Read on every plan, so a
+// tuning sweep can change it between calls.  For sweeps only: the selector's choices are
+// the measured ones.
+struct Override {
+  int kernel = -1;
+  int splits = 1;
+};
+
+Override read_override() {
+  Override o;
+  const char* env = getenv("CMPEXT3_GEMM_CONFIG");
+  if (env == nullptr) return o;
+  char buf[128];
+  snprintf(buf, sizeof buf, "%s", env);
+  for (char* tok = strtok(buf, ", "); tok != nullptr; tok = strtok(nullptr, ", ")) {
+    if (strncmp(tok, "kernel=", 7) == 0) {
+      for (int id = 0; id < kNumKernels; ++id)
+        if (strcmp(tok + 7, kernel_name((KernelId)id)) == 0) o.kernel = id;
+    } else if (strncmp(tok, "splits=", 7) == 0) {
+      const int v = atoi(tok + 7);
+      if (v >= 1 && v <= 16) o.splits = v;
+    }
+  }
+  return o;
+}
+
+// K split of a forced tile kernel: s ways (ranges of whole 64-k steps, none empty), fp32
+// partials in the workspace (N % 4 == 0 for their 16-byte stores); 1 if that does not fit.
+int forced_splits(const Request& r, int s, int64_t* ksplit) {
+  if (s <= 1 || r.N % 4 != 0 || r.K <= 0) return 1;
+  const int64_t ks = cdiv(cdiv(r.K, s), 64) * 64;
+  if ((s - 1) * ks >= r.K || (int64_t)s * r.batch * r.M * r.N * 4 > r.ws_bytes) return 1;
+  *ksplit = ks;
+  return s;
+}
+
+// Applies the override to a 16-bit plan: a tiled kernel (optionally split) when `fast`,
+// the streaming kernel when `stream_ok`, the generic kernel always.
+void override16(const Request& r, bool fast, bool stream_ok, Plan* p) {
+  const Override o = read_override();
+  if (o.kernel < 0) return;
+  Plan q{};
+  q.group_m = p->group_m;
+  q.threads = 256;
+  q.splits = 1;
+  switch (o.kernel) {
+    case kTile256x256:
+    case kTile256x224:
+    case kTile128x128:
+    case kTile64x256: {
+      if (!fast) return;
+      q.kernel = (KernelId)o.kernel;
+      q.bm = o.kernel == kTile64x256 ? 64 : o.kernel == kTile128x128 ? 128 : 256;
+      q.bn = o.kernel == kTile256x224 ? 224 : o.kernel == kTile128x128 ? 128 : 256;
+      if (q.bm == 256) q.threads = 512;
+      int64_t ks = 0;
+      if (q.bm >= 128 && (q.splits = forced_splits(r, o.splits, &ks)) > 1) {
+        q.ksplit = (int)ks;
+        q.ws_bytes = (int64_t)q.splits * r.batch * r.M * r.N * 4;
+      }
+      break;
+    }
+    case kStream64x128:
+    case kStream128x128:
+      if (!stream_ok) return;
+      q.kernel = r.M <= 64 ? kStream64x128 : kStream128x128;
+      q.bm = r.M <= 64 ? 64 : 128;
+      q.bn = 128;
+      q.threads = r.M <= 64 ? 256 : 512;
+      break;
+    case kGeneric16:
+      q.kernel = kGeneric16;
+      q.bm = 64;
+      q.bn = 64;
+      q.forced = true;  // no padded copies in its place
+      break;
+    default:
+      return;
+  }
+  *p = q;
+}
+
+// Applies the override to an fp32 plan: any fp32 tile, optionally split.
+void override32(const Request& r, bool dma16, Plan* p) {
+  const Override o = read_override();
+  if (o.kernel < 0) return;
+  for (const F32Tile& c : kTiles32) {
+    if (c.id != o.kernel) continue;
+    Plan q{};
+    q.group_m = p->group_m;
+    q.threads = 256;
+    q.kernel = c.id;
+    q.bm = c.bm;
+    q.bn = c.bn;
+    q.dma16 = dma16;
+    int64_t ks = 0;
+    if ((q.splits = forced_splits(r, o.splits, &ks)) > 1) {
+      q.ksplit = (int)ks;
+      q.ws_bytes = (int64_t)q.splits * r.batch * r.M * r.N * 4;
+    }
+    q.forced = true;  // no padded copies in its place
+    *p = q;
+  }
+}
+
 int make_plan_core(const Request& r, Plan* plan) {
   if (r.dtype != kF16 && r.dtype != kBF16 && r.dtype != kF32) return CMPEXT3_ERR_UNSUPPORTED;
   if (r.layout != kKN && r.layout != kNK) return CMPEXT3_ERR_UNSUPPORTED;
@@ -174,6 +284,7 @@ int make_plan_core(const Request& r, Plan* plan) {
       p.ksplit = (int)(cdiv(cdiv(r.K, best_s), 64) * 64);
       p.ws_bytes = best_s * r.batch * r.M * r.N * 4;
     }
+    override32(r, dma16, &p);
   } else {
     const bool skinny_ok = r.M <= 64 && r.align >= 16 && r.K % 8 == 0 &&
                            r.lda % 8 == 0 && r.N % 8 == 0 && r.ldb % 8 == 0 &&
@@ -189,6 +300,12 @@ int make_plan_core(const Request& r, Plan* plan) {
     // 64x1048576x128 118 vs 237 us, 16x262144x512 48 vs 67 us, 64x32768x128 5.5
     // vs 8.3 us).
     const bool skinny_tiles_enough = fast && cdiv(r.N, 128) * r.batch >= kNumCUs;
+    // what the streaming kernel needs (B as [K,N], one A for the batch, ...; it is chosen
+    // below only with enough tiles per workgroup)
+    const bool stream_ok = fast && r.layout == kKN && r.M <= kStreamMaxRows && r.K <= 256 && r.N % 8 == 0 &&
+                           r.ldc % 8 == 0 && (!batched || (r.stride_a == 0 && r.stride_c % 8 == 0)) &&
+                           (!r.has_bias || r.bias_row) && 128 * r.ldb * 2 <= kIntMax &&
+                           128 * r.ldc * 2 <= kIntMax && cdiv(r.N, 128) * r.batch <= kIntMax;
     if (skinny_ok && !skinny_tiles_enough && r.layout == kNK) {
       // B is [N, K] (a Linear weight): strips of W rows over all of K; 16-row
       // strips when 32-row ones would leave CUs idle.
@@ -222,11 +339,7 @@ int make_plan_core(const Request& r, Plan* plan) {
         p.kernel = kSkinny;
         p.bn = 32;
       }
-    } else if (fast && r.layout == kKN && r.M <= kStreamMaxRows && r.K <= 256 && r.N % 8 == 0 && r.ldc % 8 == 0 &&
-               (!batched || (r.stride_a == 0 && r.stride_c % 8 == 0)) && (!r.has_bias || r.bias_row) &&
-               128 * r.ldb * 2 <= kIntMax && 128 * r.ldc * 2 <= kIntMax &&
-               cdiv(r.N, 128) * r.batch * cdiv(r.M, r.M <= 64 ? 64 : 128) >= 16 * kNumCUs &&
-               cdiv(r.N, 128) * r.batch <= kIntMax) {
+    } else if (stream_ok && cdiv(r.N, 128) * r.batch * cdiv(r.M, r.M <= 64 ? 64 : 128) >= 16 * kNumCUs) {
       // Short K over many columns with one A (a 1x1 convolution: weight x every image's
       // pixels): bound by streaming B in and C out, which persistent workgroups with
       // three tiles in flight do faster than one tile per workgroup once each has >= 16
@@ -281,6 +394,7 @@ int make_plan_core(const Request& r, Plan* plan) {
       p.bm = 64;
       p.bn = 64;
     }
+    override16(r, fast, stream_ok, &p);
   }
   if (p.splits == 0) p.splits = 1;
   if (p.kernel == kSkinny || p.kernel == kSkinnyWide || p.kernel == kSkinnyNK || p.kernel == kStream64x128 ||
@@ -371,8 +485,8 @@ static int plan_f32_padded(const Request& r, Plan* plan) {
 
 int make_plan(const Request& r, Plan* plan) {
   const int st = make_plan_core(r, plan);
-  if (st == CMPEXT3_OK && r.dtype == kF32) return plan_f32_padded(r, plan);
-  if (st != CMPEXT3_OK || plan->kernel != kGeneric16) return st;
+  if (st == CMPEXT3_OK && r.dtype == kF32) return plan->forced ? st : plan_f32_padded(r, plan);
+  if (st != CMPEXT3_OK || plan->kernel != kGeneric16 || plan->forced) return st;
   const double work = (double)r.M * (double)r.N * (double)r.K * (double)r.batch;
   const int aa = r.align_a ? r.align_a : r.align, ab = r.align_b ? r.align_b : r.align;
   const int ac = r.align_c ? r.align_c : r.align;

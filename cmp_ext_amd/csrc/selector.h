@@ -28,6 +28,7 @@ struct Plan {
   int64_t stride_a_p, stride_b_p;      // their batch strides (0: one copy shared by the batch)
   int64_t pad_a_bytes, pad_b_bytes;    // workspace bytes of each copy (multiples of 256)
   bool dma16;  // fp32: rows 16-byte aligned, K (and N for B as [K,N]) multiples of 4
+  bool forced;  // chosen by the CMPEXT3_GEMM_CONFIG override (no padded copies in its place)
 };
 
 struct Request {

@@ -206,3 +206,45 @@ def test_zero_sizes_are_valid():
     for M, N, K in [(0, 5, 5), (5, 0, 5), (5, 5, 0)]:
         kid, _ = cabi.plan(cabi.F16, cabi.B_KN, M, N, K)
         assert kid >= 0
+
+
+def test_gemm_config_override(monkeypatch):
+    """CMPEXT3_GEMM_CONFIG forces a kernel (and a K split) where that kernel's requirements
+    hold for the call, and is ignored otherwise."""
+    ws = 1 << 40
+    base = cabi.plan(cabi.F16, cabi.B_KN, 2048, 2048, 2048, workspace_bytes=ws)[1]
+    monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=tile256x256,splits=2")
+    desc = cabi.plan(cabi.F16, cabi.B_KN, 2048, 2048, 2048, workspace_bytes=ws)[1]
+    assert desc.startswith("kernel=tile256x256") and "splits=2 ksplit=1024" in desc, desc
+    # the split needs the workspace for its fp32 partials: without it, the tile alone
+    desc = cabi.plan(cabi.F16, cabi.B_KN, 2048, 2048, 2048)[1]
+    assert desc.startswith("kernel=tile256x256") and "splits" not in desc, desc
+    # misaligned rows without a workspace: no tiled kernel can run them, so the override is
+    # ignored (generic); with one, the padded copies run the forced tile
+    assert cabi.plan(cabi.F16, cabi.B_KN, 2048, 2048, 2047)[1].startswith("kernel=generic64x64")
+    desc = cabi.plan(cabi.F16, cabi.B_KN, 2048, 2048, 2047, workspace_bytes=ws)[1]
+    assert desc.startswith("kernel=tile256x256") and "padded=AB" in desc, desc
+    # the streaming kernel on a product it can take, however few its tiles; not with a bias
+    # per column or B as [N, K]
+    monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=stream64x128")
+    desc = cabi.plan(cabi.F16, cabi.B_KN, 200, 1000, 96)[1]
+    assert desc.startswith("kernel=stream128x128") and "grid=1x8x1" in desc, desc
+    assert not cabi.plan(cabi.F16, cabi.B_KN, 200, 1000, 96, has_bias=True)[1].startswith("kernel=stream")
+    assert not cabi.plan(cabi.F16, cabi.B_NK, 200, 1000, 96)[1].startswith("kernel=stream")
+    assert not cabi.plan(cabi.F16, cabi.B_KN, 200, 1000, 264)[1].startswith("kernel=stream")
+    # the generic kernel, with no padded copies in its place
+    monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=generic64x64")
+    desc = cabi.plan(cabi.BF16, cabi.B_KN, 2048, 2048, 2047, workspace_bytes=ws)[1]
+    assert desc.startswith("kernel=generic64x64") and "padded" not in desc, desc
+    # fp32 tiles, split
+    monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=f32tile64x64 splits=4")
+    desc = cabi.plan(cabi.F32, cabi.B_KN, 512, 512, 4096, workspace_bytes=ws)[1]
+    assert desc.startswith("kernel=f32tile64x64 ") and "splits=4 ksplit=1024" in desc, desc
+    # an fp32 name on a 16-bit call, an unknown name, a malformed split: ignored
+    assert cabi.plan(cabi.F16, cabi.B_KN, 2048, 2048, 2048, workspace_bytes=ws)[1] == base
+    for bad in ("kernel=tile999", "kernel=", "splits=2", "kernel=tile128x128,splits=zero"):
+        monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", bad)
+        desc = cabi.plan(cabi.F16, cabi.B_KN, 2048, 2048, 2048, workspace_bytes=ws)[1]
+        assert desc == base or (bad.startswith("kernel=tile128x128") and "splits" not in desc), (bad, desc)
+    monkeypatch.delenv("CMPEXT3_GEMM_CONFIG")
+    assert cabi.plan(cabi.F16, cabi.B_KN, 2048, 2048, 2048, workspace_bytes=ws)[1] == base
