@@ -138,7 +138,8 @@ Override read_override() {
   if (env == nullptr) return o;
   char buf[128];
   snprintf(buf, sizeof buf, "%s", env);
-  for (char* tok = strtok(buf, ", "); tok != nullptr; tok = strtok(nullptr, ", ")) {
+  char* save = nullptr;  // strtok_r: plans may be made on several host threads at once
+  for (char* tok = strtok_r(buf, ", ", &save); tok != nullptr; tok = strtok_r(nullptr, ", ", &save)) {
     if (strncmp(tok, "kernel=", 7) == 0) {
       for (int id = 0; id < kNumKernels; ++id)
         if (strcmp(tok + 7, kernel_name((KernelId)id)) == 0) o.kernel = id;
