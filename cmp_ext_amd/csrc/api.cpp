@@ -66,7 +66,7 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
       return launch_tile(dtype, plan.kernel, lay, p, grid, s);
     case kStream64x128:
     case kStream128x128:
-      return launch_stream((DType)dtype, p, grid, s);
+      return launch_stream((DType)dtype, lay, p, grid, s);
     case kSkinny:
       return launch_skinny((DType)dtype, plan.mb, p, grid, s);
     case kSkinnyNK:

@@ -25,7 +25,7 @@ hipError_t launch_skinny_wide(DType dt, int mb, const GemmParams& p, float* ws, 
 hipError_t launch_skinny_reduce(DType dt, const GemmParams& p, const float* ws, int splits, int batch,
                                 hipStream_t s);
 // grid.x = 128-column tiles, grid.z = batch entries (one A shared by all, M <= 128); bias none or per row.
-hipError_t launch_stream(DType dt, const GemmParams& p, dim3 grid, hipStream_t s);
+hipError_t launch_stream(DType dt, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
 hipError_t launch_f32(KernelId id, BLayout lay, bool dma16, const GemmParams& p, dim3 grid, hipStream_t s);
 hipError_t launch_generic(DType dt, BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s);
 // dst[b][r][c] = src[b][r][c] (elements of esz = 2 or 4 bytes) for r < rows, c < cols,

@@ -216,6 +216,9 @@ std::vector<int64_t> expand_param(const py::object& v) {
 // linear on a contiguous copy + permute back into a second copy; here every
 // image is one GEMM out_b = W * in_b on the NCHW data as it lies, with the
 // bias added per output channel in the epilogue, all images in one launch.
+// A channels-last input is read in place (B given as [H*W, C_in] per image), as the
+// reference's permute to NHWC makes it contiguous at no cost there (:407); the output is
+// NCHW-contiguous either way, as the reference's (:423).
 // The reference's general direct-convolution kernels (launch_conv2d_*, :458-488)
 // are not part of this library: any other kernel size, stride, padding or
 // dilation raises.
@@ -247,7 +250,10 @@ torch::Tensor conv2d(torch::Tensor input, torch::Tensor weight, c10::optional<to
   checked_int(Cout, "C_out");
   const int64_t hw = checked_int(H * W, "H*W");
   c10::DeviceGuard guard(input.device());
-  input = input.contiguous();
+  // A channels-last (NHWC) input is read as it lies: image b is then [H*W, C_in], B given as
+  // [N, K]; any other layout is made NCHW-contiguous.
+  const bool nhwc = !input.is_contiguous() && input.is_contiguous(at::MemoryFormat::ChannelsLast);
+  if (!nhwc) input = input.contiguous();
   weight = weight.contiguous();
   const void* bias_ptr = nullptr;
   torch::Tensor bias_c;
@@ -262,9 +268,14 @@ torch::Tensor conv2d(torch::Tensor input, torch::Tensor weight, c10::optional<to
   }
   torch::Tensor out = torch::empty({Bn, Cout, H, W}, input.options());
   // the GEMMs of cmpext3_conv2d_1x1: out_b[C_out, HW] = W[C_out, C_in] * in_b[C_in, HW] for
-  // every image b, the weight shared (stride 0), the bias per output row
-  gemm(code, CMPEXT3_B_KN, weight, std::max<int64_t>(Cin, 1), 0, input, std::max<int64_t>(hw, 1), Cin * hw, out,
-       std::max<int64_t>(hw, 1), Cout * hw, bias_ptr, CMPEXT3_BIAS_PER_ROW, Cout, hw, Cin, Bn, "conv2d");
+  // every image b, the weight shared (stride 0), the bias per output row; from an NHWC
+  // input, out_b = W * (in_b[HW, C_in])^T
+  if (nhwc)
+    gemm(code, CMPEXT3_B_NK, weight, std::max<int64_t>(Cin, 1), 0, input, std::max<int64_t>(Cin, 1), hw * Cin,
+         out, std::max<int64_t>(hw, 1), Cout * hw, bias_ptr, CMPEXT3_BIAS_PER_ROW, Cout, hw, Cin, Bn, "conv2d");
+  else
+    gemm(code, CMPEXT3_B_KN, weight, std::max<int64_t>(Cin, 1), 0, input, std::max<int64_t>(hw, 1), Cin * hw,
+         out, std::max<int64_t>(hw, 1), Cout * hw, bias_ptr, CMPEXT3_BIAS_PER_ROW, Cout, hw, Cin, Bn, "conv2d");
   return out;
 }
 

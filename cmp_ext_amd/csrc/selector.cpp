@@ -301,9 +301,9 @@ int make_plan_core(const Request& r, Plan* plan) {
     // 64x1048576x128 118 vs 237 us, 16x262144x512 48 vs 67 us, 64x32768x128 5.5
     // vs 8.3 us).
     const bool skinny_tiles_enough = fast && cdiv(r.N, 128) * r.batch >= kNumCUs;
-    // what the streaming kernel needs (B as [K,N], one A for the batch, ...; it is chosen
-    // below only with enough tiles per workgroup)
-    const bool stream_ok = fast && r.layout == kKN && r.M <= kStreamMaxRows && r.K <= 256 && r.N % 8 == 0 &&
+    // what the streaming kernel needs (one A for the batch, C's rows in 16-byte pieces, ...;
+    // B as [K,N] or [N,K]; it is chosen below only with enough tiles per workgroup)
+    const bool stream_ok = fast && r.M <= kStreamMaxRows && r.K <= 256 && r.N % 8 == 0 &&
                            r.ldc % 8 == 0 && (!batched || (r.stride_a == 0 && r.stride_c % 8 == 0)) &&
                            (!r.has_bias || r.bias_row) && 128 * r.ldb * 2 <= kIntMax &&
                            128 * r.ldc * 2 <= kIntMax && cdiv(r.N, 128) * r.batch <= kIntMax;

@@ -53,7 +53,10 @@ constexpr int kStreamStorePolicy = 2;
 // WG: groups of 4 waves, group g computing rows 64 g .. 64 g + 63 of the tile (MT = 64 WG
 // rows, M <= MT); KC: chunks of 128 k per tile (K <= 128 KC).
 // NT: B read with the non-temporal cache policy (for read-dominated products).
-template <typename T, int BIAS, int WG, int KC, bool NT>
+// BNK: B given as [N, K] (rows of K; e.g. an NHWC image: pixels x input channels), stored
+// in a slot as [n][k] (rows of 256 bytes, 16-byte chunks XOR-swizzled by n % 16) and read
+// with ds_read_b128; otherwise B is [K, N], stored [k][n] and read with transposing reads.
+template <typename T, int BIAS, int WG, int KC, bool NT, bool BNK>
 __global__ void __launch_bounds__(256 * WG, 1) gemm_stream_kernel(const GemmParams p, int total_tiles) {
   static_assert((WG == 1 || WG == 2) && (KC == 1 || KC == 2), "tile shapes");
   constexpr int RW = 64;                         // rows per wave
@@ -121,17 +124,25 @@ __global__ void __launch_bounds__(256 * WG, 1) gemm_stream_kernel(const GemmPara
 #pragma unroll
   for (int i = 0; i < FM; ++i) asm volatile("" : "+v"(bias_m[i]));
 
-  // ---- DMA: piece q of wave w fills bytes (w*P + q) KiB of a slot = k rows 4(wP+q) .. +3
-  // of the chunk ----
+  // ---- DMA: piece q of wave w fills bytes (w*P + q) KiB of a slot: k rows 4(wP+q) .. +3
+  // of the chunk ([K, N]), or n rows 4(wP+q) .. +3 ([N, K]; lane l: row 4(wP+q) + l/16,
+  // 16-byte chunk position l % 16, holding k = 8 ((l % 16) ^ (n % 16)) .. +7) ----
   // b_off[h][q]: the piece's offset in chunk h of a tile, or kBufOOB past K
   uint32_t b_off[KC][P];
   int b_n[P];
 #pragma unroll
   for (int q = 0; q < P; ++q) {
     int k, n;
-    dma_kn_geom(wave * P + q, lane, PITCH, k, n);
+    if constexpr (BNK) {
+      const int pos = (wave * P + q) * 1024 + 16 * lane;
+      n = pos / PITCH;
+      k = 8 * (((pos % PITCH) >> 4) ^ (n & 15));
+    } else {
+      dma_kn_geom(wave * P + q, lane, PITCH, k, n);
+    }
 #pragma unroll
-    for (int h = 0; h < KC; ++h) b_off[h][q] = kStreamKC * h + k < K ? (uint32_t)(k * p.ldb + n) * 2u : kBufOOB;
+    for (int h = 0; h < KC; ++h)
+      b_off[h][q] = kStreamKC * h + k < K ? (uint32_t)(BNK ? n * p.ldb + k : k * p.ldb + n) * 2u : kBufOOB;
     b_n[q] = n;
   }
   const uint32_t lds_w = lds_addr(smem) + (uint32_t)(wave * P * 1024);
@@ -143,7 +154,8 @@ __global__ void __launch_bounds__(256 * WG, 1) gemm_stream_kernel(const GemmPara
     const bool live = c < nchunks;
     const int t = live ? me + (c / KC) * step : 0;
     const int bz = t / tiles_n, n0 = (t - bz * tiles_n) * kStreamN;
-    i32x4 r = make_rsrc_sgpr((const T*)p.B + (int64_t)bz * p.stride_b + (int64_t)(kStreamKC * h) * p.ldb + n0);
+    i32x4 r = make_rsrc_sgpr((const T*)p.B + (int64_t)bz * p.stride_b +
+                             (BNK ? (int64_t)n0 * p.ldb + kStreamKC * h : (int64_t)(kStreamKC * h) * p.ldb + n0));
     r[2] = live ? (int)kBufRecords : 0;
     const uint32_t base = lds_w + (uint32_t)((c % SLOTS) * SLOT);
     static_for<P>([&](auto qc) {
@@ -156,11 +168,14 @@ __global__ void __launch_bounds__(256 * WG, 1) gemm_stream_kernel(const GemmPara
     });
   };
 
-  // ---- fragment addresses ([k][n] slot, transposing reads as in the tile kernel) ----
+  // ---- fragment addresses: [k][n] slot, transposing reads as in the tile kernel; [n][k]
+  // slot, row n = 32 wc + 16 j + r16 (its chunk position added per sub-step) ----
   uint32_t fb_off[FN];
   const int kr = 8 * G + (r16 >> 2);
 #pragma unroll
-  for (int j = 0; j < FN; ++j) fb_off[j] = kn_off(kr, PITCH, (32 * wc + 16 * j + 4 * (r16 & 3)) * 2);
+  for (int j = 0; j < FN; ++j)
+    fb_off[j] = BNK ? (uint32_t)((32 * wc + 16 * j + r16) * PITCH)
+                    : kn_off(kr, PITCH, (32 * wc + 16 * j + 4 * (r16 & 3)) * 2);
 
   // ---- results: after one permlane16 swap per dword, lane (r16, G) holds row RW grp + 16i + r16,
   // columns col .. col+7 of the tile; they go to staging buffer i % 2 as 16-byte chunk
@@ -226,20 +241,28 @@ __global__ void __launch_bounds__(256 * WG, 1) gemm_stream_kernel(const GemmPara
       static_for<KSC>([&](auto sc) {  // sub-steps of 32 k: B fragments, then their MFMAs
         constexpr int s = decltype(sc)::value;
         u32x4 fb[FN];
-        static_for<FN * 2>([&](auto rc) {
-          constexpr int r = decltype(rc)::value, j = r / 2, half = r % 2;
-          typedef short s16x4 __attribute__((ext_vector_type(4)));
-          const unsigned char* q = sb + fb_off[j] + (32 * s + 4 * half) * PITCH;
-          const u32x2 v = __builtin_bit_cast(
-              u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q));
-          if constexpr (half == 0) {
-            fb[j].x = v.x;
-            fb[j].y = v.y;
-          } else {
-            fb[j].z = v.x;
-            fb[j].w = v.y;
-          }
-        });
+        if constexpr (BNK) {
+          // k = 32 s + 8 G .. +7 of row n: chunk 4 s + G at position (4 s + G) ^ (n % 16),
+          // n % 16 = r16 (16 distinct positions across the 16 rows: conflict free)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            fb[j] = *(const u32x4*)(sb + fb_off[j] + (((4 * s + G) ^ r16) << 4));
+        } else {
+          static_for<FN * 2>([&](auto rc) {
+            constexpr int r = decltype(rc)::value, j = r / 2, half = r % 2;
+            typedef short s16x4 __attribute__((ext_vector_type(4)));
+            const unsigned char* q = sb + fb_off[j] + (32 * s + 4 * half) * PITCH;
+            const u32x2 v = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q));
+            if constexpr (half == 0) {
+              fb[j].x = v.x;
+              fb[j].y = v.y;
+            } else {
+              fb[j].z = v.x;
+              fb[j].w = v.y;
+            }
+          });
+        }
         static_for<FM * FN>([&](auto xc) {
           constexpr int x = decltype(xc)::value, ii = x / FN, j = x % FN;
           acc[ii][j] = Mfma<T>::mma(fb[j], fa[ii][KSC * h + s], acc[ii][j]);

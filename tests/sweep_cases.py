@@ -63,8 +63,8 @@ def draw_case(rng: np.random.Generator, idx: int) -> dict:
 
 
 def draw_stream_case(rng: np.random.Generator, idx: int, wide_rows: bool) -> dict:
-    """A 1x1-convolution-shaped case: one A for the batch, B as [K,N], >= 4096 column tiles
-    (M of 65 to 320 if wide_rows)."""
+    """A 1x1-convolution-shaped case: one A for the batch, B as [K,N] (or [N,K] for every
+    third case), >= 4096 column tiles (M of 65 to 320 if wide_rows)."""
     dtype = ["fp16", "bf16"][rng.integers(2)]
     M = int(rng.integers(65, 321)) if wide_rows else int(rng.integers(1, 65))
     K = int(rng.choice([8, 64, 72, 128, 136, 200, 256]))
@@ -72,9 +72,13 @@ def draw_stream_case(rng: np.random.Generator, idx: int, wide_rows: bool) -> dic
     batch = -(-4096 // -(-N // 128))
     ldb = N + int(rng.choice([0, 8]))
     ldc = N + int(rng.choice([0, 8]))
-    return dict(idx=idx, dtype=dtype, layout=cabi.B_KN, M=M, N=N, K=K, lda=K + int(rng.choice([0, 8])), ldb=ldb,
+    layout = cabi.B_NK if idx % 3 == 2 else cabi.B_KN  # every third as NHWC images: B given as [N, K]
+    if layout == cabi.B_NK:
+        ldb = K + int(rng.choice([0, 8]))
+    rows_b = K if layout == cabi.B_KN else N
+    return dict(idx=idx, dtype=dtype, layout=layout, M=M, N=N, K=K, lda=K + int(rng.choice([0, 8])), ldb=ldb,
                 ldc=ldc, off_a=0, off_b=int(rng.choice([0, 8])), off_c=int(rng.choice([0, 8])), batch=batch,
-                stride_a=0, stride_b=K * ldb + int(rng.choice([0, 8])), stride_c=M * ldc + int(rng.choice([0, 8])),
+                stride_a=0, stride_b=rows_b * ldb + int(rng.choice([0, 8])), stride_c=M * ldc + int(rng.choice([0, 8])),
                 bias=["row", None][rng.integers(2)], off_bias=0, workspace=bool(rng.integers(2)),
                 sample=sorted({0, batch // 2, batch - 1}))
 

@@ -72,6 +72,26 @@ def test_conv2d_1x1_matches_oracle(dtype, shape):
     assert O.rel_frobenius(O.to_f64(out_nb.cpu()), oracle(x, w, None)) <= O.TOLERANCE[dtype]
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("shape", [(8, 64, 256, 256, 48), (16, 192, 128, 256, 96), (16, 96, 128, 256, 320),
+                                   (2, 40, 5, 9, 24)])
+def test_conv2d_1x1_channels_last(dtype, shape):
+    """NHWC (channels-last) inputs are read in place (B given as [H*W, C_in] per image; the
+    streaming kernel for the large shapes): same result as the NCHW input, NCHW output."""
+    B, C, H, W, Co = shape
+    x, w, bias = make(dtype, B, C, H, W, Co, seed=sum(shape) + 1)
+    xg = x.cuda().to(memory_format=torch.channels_last)
+    assert not xg.is_contiguous() and xg.is_contiguous(memory_format=torch.channels_last)
+    print(f"conv2d channels-last {dtype} {shape}", flush=True)
+    out = cmpext3.conv2d(xg, w.cuda(), bias.cuda())
+    print(f"  ran: {cmpext3.last_plan()}", flush=True)
+    torch.cuda.synchronize()
+    assert out.shape == (B, Co, H, W) and out.is_contiguous()
+    if dtype != "fp32":
+        assert "layout=NK" in cmpext3.last_plan()
+    assert O.rel_frobenius(O.to_f64(out.cpu()), oracle(x, w, bias)) <= O.TOLERANCE[dtype]
+
+
 @pytest.mark.parametrize("name", ["conv_f16_2x5x3x4_o6_bias", "conv_bf16_3x24x2x5_o7",
                                   "conv_f32_1x9x4x4_o3_bias"])
 def test_conv2d_golden_fixtures(golden, name):

@@ -794,6 +794,54 @@ def test_stream_kernel(dtype, M, N, K, batch, bias):
         assert torch.equal(c, c2)
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("M,N,K,batch,bias", [
+    (64, 16384, 128, 32, True),    # NHWC images of 128 x 128 pixels, 128 -> 64 channels
+    (40, 8200, 72, 64, False),     # ragged M, N (last tile 8 pixels) and K
+    (1, 524288, 8, 1, False),      # one row; 16-byte rows of B
+    (128, 16384, 256, 32, True),   # 128-row tiles, two K chunks
+    (300, 8200, 136, 32, False),   # three row blocks, the second chunk of 8 k
+])
+def test_stream_kernel_b_nk(dtype, M, N, K, batch, bias):
+    """The streaming kernel with B given as [N, K] (a 1x1 convolution over NHWC images:
+    pixels x input channels) through the C ABI, against the float64 oracle on sampled
+    batch entries and an fp32 GPU product on all, deterministic."""
+    g = torch.Generator().manual_seed(M + K + batch + 1)
+    a = (torch.randn(M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    b = torch.randn(batch, N, K, generator=g).to(DT[dtype])
+    bvec = torch.randn(M, generator=g).to(DT[dtype]) if bias else None
+    ag, bg = a.cuda(), b.cuda()
+    bvg = bvec.cuda() if bias else None
+    c = torch.full((batch, M, N), float("nan"), dtype=DT[dtype], device="cuda")
+    print(f"stream NK {dtype} M={M} N={N} K={K} batch={batch} bias={bias}", flush=True)
+    st, call = cabi.prepare(CODE[dtype], cabi.B_NK, ag, K, 0, bg, K, N * K, c, N, M * N, bvg, M, N, K, batch,
+                            cabi.BIAS_PER_ROW if bias else 0, 0)
+    assert st == cabi.OK
+    _, desc = cabi.describe(call)
+    SEEN_KERNELS.add(kernel_of(desc))
+    assert kernel_of(desc) == ("stream64x128" if M <= 64 else "stream128x128") and "layout=NK" in desc, desc
+    assert cabi.run(call) == cabi.OK
+    torch.cuda.synchronize()
+    assert not torch.isnan(c).any()
+    ref = torch.matmul(ag.float(), bg.float().transpose(1, 2))
+    if bias:
+        ref = ref + bvg.float()[:, None]
+    e2 = ((c.double() - ref.double()).norm() / ref.double().norm()).item()
+    assert e2 <= O.TOLERANCE[dtype]
+    for i in sorted({0, batch // 2, batch - 1}):
+        r = O.matmul_f64(O.to_f64(a), O.to_f64(b[i]).T)
+        if bias:
+            r = r + O.to_f64(bvec)[:, None]
+        assert O.rel_frobenius(O.to_f64(c[i].cpu()), r) <= O.TOLERANCE[dtype], i
+    c2 = torch.full_like(c, float("nan"))
+    assert cabi.run(call) == cabi.OK
+    torch.cuda.synchronize()
+    c2.copy_(c)
+    assert cabi.run(call) == cabi.OK
+    torch.cuda.synchronize()
+    assert torch.equal(c, c2)
+
+
 def test_every_kernel_family_was_exercised():
     missing = set(KERNEL_NAMES) - SEEN_KERNELS
     assert not missing, f"kernels never selected by these tests: {missing}"

@@ -51,13 +51,14 @@ def test_skinny_m_batches_with_many_tiles_go_tiled():
 
 
 def _prepared_kernel(dtype, M, N, K, batch, stride_a, flags=0, bias=None, lda=None, ldc=None, align=0,
-                     workspace_limit=0):
+                     workspace_limit=0, layout=cabi.B_KN):
     """Kernel id and description the C ABI plans for these pointers and pitches (no GPU:
-    prepare only; by default without a workspace)."""
+    prepare only; by default without a workspace; B packed, as [K, N] or [N, K])."""
     lda = lda or K
     ldc = ldc or N
+    ldb = N if layout == cabi.B_KN else K
     a, b, c = 0x100000 + align, 0x40000000, 0x80000000
-    st, call = cabi.prepare(dtype, cabi.B_KN, a, lda, stride_a, b, N, K * N, c, ldc, M * ldc, bias, M, N, K,
+    st, call = cabi.prepare(dtype, layout, a, lda, stride_a, b, ldb, K * N, c, ldc, M * ldc, bias, M, N, K,
                             batch, flags, workspace_limit)
     assert st == cabi.OK
     return cabi.describe(call)
@@ -84,6 +85,11 @@ def test_stream_kernel_for_convolution_shapes():
     kid, desc = _prepared_kernel(cabi.F16, 65, 16384, 128, 64, 0)
     assert kid == K_STREAM128 and "tile=128x128" in desc, desc   # 65..128 rows: 128-row tiles
     assert _prepared_kernel(cabi.BF16, 128, 16384, 128, 64, 0, cabi.BIAS_PER_ROW, bias=0x1000)[0] == K_STREAM128
+    # B as [N, K] (NHWC images: pixels x input channels), the same rules
+    kid, desc = _prepared_kernel(cabi.F16, 64, 16384, 128, 64, 0, cabi.BIAS_PER_ROW, bias=0x1000, layout=cabi.B_NK)
+    assert kid == K_STREAM and "layout=NK" in desc, desc
+    assert _prepared_kernel(cabi.BF16, 200, 16384, 256, 32, 0, layout=cabi.B_NK)[0] == K_STREAM128
+    assert _prepared_kernel(cabi.F16, 64, 16384, 264, 64, 0, layout=cabi.B_NK)[0] != K_STREAM
     # more than 128 rows: row blocks of 128, up to 2048 rows; the grid counts column tiles
     # only (the kernel walks its row blocks itself): 128 tiles x 1 x 32 images
     assert _prepared_kernel(cabi.F16, 129, 16384, 128, 64, 0)[0] == K_STREAM128
@@ -224,13 +230,13 @@ def test_gemm_config_override(monkeypatch):
     assert cabi.plan(cabi.F16, cabi.B_KN, 2048, 2048, 2047)[1].startswith("kernel=generic64x64")
     desc = cabi.plan(cabi.F16, cabi.B_KN, 2048, 2048, 2047, workspace_bytes=ws)[1]
     assert desc.startswith("kernel=tile256x256") and "padded=AB" in desc, desc
-    # the streaming kernel on a product it can take, however few its tiles; not with a bias
-    # per column or B as [N, K]
+    # the streaming kernel on a product it can take, however few its tiles (B as [K, N] or
+    # [N, K]); not with a bias per column or K above 256
     monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=stream64x128")
     desc = cabi.plan(cabi.F16, cabi.B_KN, 200, 1000, 96)[1]
     assert desc.startswith("kernel=stream128x128") and "grid=1x8x1" in desc, desc
     assert not cabi.plan(cabi.F16, cabi.B_KN, 200, 1000, 96, has_bias=True)[1].startswith("kernel=stream")
-    assert not cabi.plan(cabi.F16, cabi.B_NK, 200, 1000, 96)[1].startswith("kernel=stream")
+    assert cabi.plan(cabi.F16, cabi.B_NK, 200, 1000, 96)[1].startswith("kernel=stream128x128")
     assert not cabi.plan(cabi.F16, cabi.B_KN, 200, 1000, 264)[1].startswith("kernel=stream")
     # the generic kernel, with no padded copies in its place
     monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=generic64x64")
