@@ -71,12 +71,28 @@ void gemm(int code, int layout, const torch::Tensor& a, int64_t lda, int64_t str
 
 // A 2-D operand usable as row-major with unit inner stride: returns the row
 // pitch, or -1 if a copy is needed.
+// Row pitches the kernels can address from a tile's base with 32-bit byte offsets (256 rows
+// of 4-byte elements); a view with a larger pitch is copied instead.
+constexpr int64_t kMaxPitch = INT_MAX / (256 * 4);
+
 int64_t row_pitch(const torch::Tensor& t) {
   const int64_t rows = t.size(0), cols = t.size(1);
   if (cols > 1 && t.stride(1) != 1) return -1;
   if (rows <= 1) return std::max<int64_t>(cols, 1);
-  if (t.stride(0) < std::max<int64_t>(cols, 1)) return -1;
+  if (t.stride(0) < std::max<int64_t>(cols, 1) || t.stride(0) > kMaxPitch) return -1;
   return t.stride(0);
+}
+
+// A 3-D operand [batch, rows, cols] whose matrices are row-major with unit inner stride:
+// sets the row pitch and the batch stride (>= 0; batch entries may overlap, as in an
+// expanded view, since operands are only read) and returns true; false if a copy is needed.
+bool batch_rows(const torch::Tensor& t, int64_t& ld, int64_t& stride) {
+  const int64_t rows = t.size(1), cols = t.size(2);
+  if (cols > 1 && t.stride(2) != 1) return false;
+  ld = rows <= 1 ? std::max<int64_t>(cols, 1) : t.stride(1);
+  if (ld < std::max<int64_t>(cols, 1) || ld > kMaxPitch || t.stride(0) < 0) return false;
+  stride = t.stride(0);
+  return true;
 }
 
 // C = A[M,K] * B[K,N].  B may also be a transposed view of a row-major
@@ -144,13 +160,35 @@ torch::Tensor linear(torch::Tensor input, const torch::Tensor& weight, c10::opti
   TORCH_CHECK(input.size(-1) == K, "Input shape mismatch with Weight");
   TORCH_CHECK(input.is_cuda(), "cmpext3.linear: tensors must be on a GPU");
   c10::DeviceGuard guard(input.device());
-  input = input.contiguous();
-  const torch::Tensor w = weight.contiguous();
   int64_t M = 1;
   for (int64_t d = 0; d + 1 < input.dim(); ++d) M *= input.size(d);
   checked_int(M, "M");
   checked_int(N, "N");
   checked_int(K, "K");
+  // x as [M, K]: a 2-D input with rows of unit stride is read in place (its row pitch as
+  // lda); any other non-contiguous input is copied
+  torch::Tensor x = input;
+  int64_t lda = input.dim() == 2 ? row_pitch(input) : -1;
+  if (lda < 0) {
+    x = input.contiguous().view({M, K});
+    lda = std::max<int64_t>(K, 1);
+  }
+  // the weight read in place: [N, K] rows (B given as [N, K]), or a transposed view of a
+  // [K, N] tensor (B given as [K, N]); otherwise copied
+  torch::Tensor w = weight;
+  int layout = CMPEXT3_B_NK;
+  int64_t ldb = row_pitch(weight);
+  if (ldb < 0) {
+    const torch::Tensor wt = weight.t();  // [K, N]
+    ldb = row_pitch(wt);
+    if (ldb >= 0) {
+      layout = CMPEXT3_B_KN;
+      w = wt;
+    } else {
+      w = weight.contiguous();
+      ldb = std::max<int64_t>(K, 1);
+    }
+  }
   const void* bias_ptr = nullptr;
   torch::Tensor bias_c;
   if (bias.has_value() && bias->defined()) {
@@ -165,8 +203,7 @@ torch::Tensor linear(torch::Tensor input, const torch::Tensor& weight, c10::opti
   std::vector<int64_t> out_shape(input.sizes().begin(), input.sizes().end() - 1);
   out_shape.push_back(N);
   torch::Tensor out = torch::empty(out_shape, input.options());
-  gemm(code, CMPEXT3_B_NK, input, std::max<int64_t>(K, 1), 0, w, std::max<int64_t>(K, 1), 0, out,
-       std::max<int64_t>(N, 1), 0, bias_ptr, 0, M, N, K, 1, "linear");
+  gemm(code, layout, x, lda, 0, w, ldb, 0, out, std::max<int64_t>(N, 1), 0, bias_ptr, 0, M, N, K, 1, "linear");
   return out;
 }
 
@@ -190,10 +227,28 @@ torch::Tensor bmm(torch::Tensor input, torch::Tensor mat2) {
   checked_int(N, "N");
   checked_int(K, "K");
   c10::DeviceGuard guard(input.device());
-  input = input.contiguous();
-  mat2 = mat2.contiguous();
+  // Operands read in place where their matrices have rows of unit stride: input as
+  // [M, K] rows (its row pitch and batch stride), mat2 as [K, N] rows or as a transposed
+  // view of [N, K] rows (B given as [N, K], e.g. the keys of Q K^T); otherwise copied.
+  int64_t lda = 0, stride_a = 0;
+  if (!batch_rows(input, lda, stride_a)) {
+    input = input.contiguous();
+    lda = std::max<int64_t>(K, 1);
+    stride_a = M * K;
+  }
+  int layout = CMPEXT3_B_KN;
+  int64_t ldb = 0, stride_b = 0;
+  if (!batch_rows(mat2, ldb, stride_b)) {
+    if (batch_rows(mat2.transpose(1, 2), ldb, stride_b)) {
+      layout = CMPEXT3_B_NK;
+    } else {
+      mat2 = mat2.contiguous();
+      ldb = std::max<int64_t>(N, 1);
+      stride_b = K * N;
+    }
+  }
   torch::Tensor out = torch::empty({Bn, M, N}, input.options());
-  gemm(code, CMPEXT3_B_KN, input, std::max<int64_t>(K, 1), M * K, mat2, std::max<int64_t>(N, 1), K * N, out,
+  gemm(code, layout, input, lda, Bn > 1 ? stride_a : 0, mat2, ldb, Bn > 1 ? stride_b : 0, out,
        std::max<int64_t>(N, 1), M * N, nullptr, 0, M, N, K, Bn, "bmm");
   return out;
 }

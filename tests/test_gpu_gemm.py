@@ -842,6 +842,45 @@ def test_stream_kernel_b_nk(dtype, M, N, K, batch, bias):
     assert torch.equal(c, c2)
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_views_read_in_place(dtype):
+    """bmm and linear read row-pitched views, batch slices and transposed operands in
+    place (the plan shows the layout and pitch they ran with) and match the oracle."""
+    g = torch.Generator().manual_seed(21)
+    dt = DT[dtype]
+    # bmm(q, k^T): the keys as a transposed view -> B given as [N, K]
+    q = (torch.randn(4, 96, 64, generator=g) / 8).to(dt).cuda()
+    k = torch.randn(4, 200, 64, generator=g).to(dt).cuda()
+    out = cmpext3.bmm(q, k.transpose(1, 2))
+    plan = cmpext3.last_plan()
+    assert "layout=NK" in plan, plan
+    ref = O.bmm_f64(O.to_f64(q.cpu()), O.to_f64(k.cpu()).transpose(0, 2, 1))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    # bmm on column slices of wider tensors (row pitch above the width) and a batch slice
+    big_a = (torch.randn(5, 96, 80, generator=g) / 8).to(dt).cuda()
+    big_b = torch.randn(5, 64, 136, generator=g).to(dt).cuda()
+    a, b = big_a[1:, :, 8:72], big_b[1:, :, :128]
+    out = cmpext3.bmm(a, b)
+    assert "layout=KN" in cmpext3.last_plan()
+    ref = O.bmm_f64(O.to_f64(a.cpu()), O.to_f64(b.cpu()))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    # linear: the weight as a transposed view of a [K, N] tensor -> B given as [K, N]; a
+    # row-pitched 2-D input
+    w_kn = (torch.randn(64, 120, generator=g) / 8).to(dt).cuda()
+    x = torch.randn(50, 72, generator=g).to(dt).cuda()[:, :64]
+    bias = torch.randn(120, generator=g).to(dt).cuda()
+    out = cmpext3.linear(x, w_kn.t(), bias)
+    assert "layout=KN" in cmpext3.last_plan()
+    ref = O.linear_f64(O.to_f64(x.cpu()), O.to_f64(w_kn.t().cpu()), O.to_f64(bias.cpu()))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    # linear with a row slice of a larger weight ([N, K] rows, B given as [N, K], offset base)
+    w_big = (torch.randn(130, 64, generator=g) / 8).to(dt).cuda()
+    out = cmpext3.linear(x, w_big[3:123])
+    assert "layout=NK" in cmpext3.last_plan()
+    ref = O.linear_f64(O.to_f64(x.cpu()), O.to_f64(w_big[3:123].cpu()))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+
+
 def test_every_kernel_family_was_exercised():
     missing = set(KERNEL_NAMES) - SEEN_KERNELS
     assert not missing, f"kernels never selected by these tests: {missing}"
