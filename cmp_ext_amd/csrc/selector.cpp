@@ -309,11 +309,17 @@ int make_plan_core(const Request& r, Plan* plan) {
                            128 * r.ldc * 2 <= kIntMax && cdiv(r.N, 128) * r.batch <= kIntMax;
     if (skinny_ok && !skinny_tiles_enough && r.layout == kNK) {
       // B is [N, K] (a Linear weight): strips of W rows over all of K; 16-row
-      // strips when 32-row ones would leave CUs idle.
+      // strips when 32-row ones would leave CUs idle.  With more than 16 rows of A every
+      // workgroup re-reads all of A from L2 (for 64 x 4096: twice W's bytes over 448 strips
+      // of a 14336-row W), so 64-row strips there once they still give >= 192 workgroups
+      // (MI355X, x[M, 4096] W[14336, 4096]^T: M = 32 27.7 -> 23.9 us, 48 30.2 -> 26.8, 64
+      // 34.1 -> 29.3; x[64, 8192] W[14336, 8192]^T 56.8 -> 51.6; x[64, 8192]
+      // W[28672, 8192]^T 111 either way).
       p.mb = (int)std::max<int64_t>(1, cdiv(r.M, 16));
       p.bm = 16 * p.mb;
       p.kernel = kSkinnyNK;
       p.bn = cdiv(r.N, 32) * std::min<int64_t>(r.batch, 65535) >= kNumCUs ? 32 : 16;
+      if (p.mb >= 2 && cdiv(r.N, 64) * std::min<int64_t>(r.batch, 65535) >= 192) p.bn = 64;
     } else if (skinny_ok && !skinny_tiles_enough) {
       p.mb = (int)std::max<int64_t>(1, cdiv(r.M, 16));
       p.bm = 16 * p.mb;

@@ -39,11 +39,13 @@ bool stream_once(int64_t rows, int64_t cols, int64_t stride, unsigned batch) {
 template <typename T, int SW, bool NT>
 hipError_t launch_nk(int mb, const GemmParams& p, dim3 grid, hipStream_t s) {
   const dim3 block(256);
-  switch (mb) {  // 1 KB of each W row per stage for one 16-row block of A, 512 bytes otherwise
-    case 1: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 1, SW, 512, NT>), grid, block, 0, s, p); break;
+  // 1 KiB of each W row per stage for one 16-row block of A, 512 bytes otherwise; 64-row
+  // strips: 512 bytes for one or two blocks, 256 for three or four (the ring keeps >= 3 stages)
+  switch (mb) {
+    case 1: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 1, SW, SW == 64 ? 256 : 512, NT>), grid, block, 0, s, p); break;
     case 2: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 2, SW, 256, NT>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 3, SW, 256, NT>), grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, SW, 256, NT>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 3, SW, SW == 64 ? 128 : 256, NT>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, SW, SW == 64 ? 128 : 256, NT>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -52,6 +54,7 @@ template <typename T>
 hipError_t launch_nk(int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {
   const bool nt = stream_once(p.N, p.K, p.stride_b, grid.z);
   if (strip == 16) return nt ? launch_nk<T, 16, true>(mb, p, grid, s) : launch_nk<T, 16, false>(mb, p, grid, s);
+  if (strip == 64) return nt ? launch_nk<T, 64, true>(mb, p, grid, s) : launch_nk<T, 64, false>(mb, p, grid, s);
   return nt ? launch_nk<T, 32, true>(mb, p, grid, s) : launch_nk<T, 32, false>(mb, p, grid, s);
 }
 }  // namespace

@@ -319,6 +319,27 @@ def test_skinny_linear_weight_binding_and_c_abi(dtype):
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("M,N,K,bias", [(24, 14336, 4096, True), (33, 12800, 2056, False), (64, 14336, 4096, True)])
+def test_skinny_nk_wide_strips(dtype, M, N, K, bias):
+    """Decode-shaped Linear with 17..64 rows of x and a tall W: 64-row W strips (two to
+    four 16-row blocks of x, 128- or 256-k stages), ragged M and K, with and without a
+    column bias, against the oracle; deterministic."""
+    g = torch.Generator().manual_seed(M + K)
+    x = (torch.randn(M, K, generator=g) / np.sqrt(K)).to(DT[dtype])
+    w = torch.randn(N, K, generator=g).to(DT[dtype])
+    b = torch.randn(N, generator=g).to(DT[dtype]) if bias else None
+    print(f"skinny_nk {dtype} M={M} N={N} K={K} bias={bias}", flush=True)
+    out = cmpext3.linear(x.cuda(), w.cuda(), None if b is None else b.cuda())
+    name, desc = launched()
+    assert name == "skinny_nk" and "x64 " in desc, desc
+    torch.cuda.synchronize()
+    ref = O.linear_f64(O.to_f64(x), O.to_f64(w), None if b is None else O.to_f64(b))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    again = cmpext3.linear(x.cuda(), w.cuda(), None if b is None else b.cuda())
+    assert torch.equal(out, again)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_weight_layout_batched_and_bias_c_abi(dtype):
     """[N, K] B through the C ABI: a batch of decode-shaped products (skinny_nk, one
     launch over grid.z) equal per entry to the single products, and a short-K product

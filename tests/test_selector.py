@@ -119,8 +119,13 @@ def test_skinny_linear_weight_layout():
     assert cabi.workspace_size(cabi.F16, cabi.B_NK, 16, 4096, 14336) == 0
     kid, desc = cabi.plan(cabi.F16, cabi.B_NK, 16, 4096, 14336, workspace_bytes=1 << 30)
     assert kid == K_SKINNY_NK and "tile=16x16" in desc and "grid=1x256x1" in desc, desc
+    kid, desc = cabi.plan(cabi.BF16, cabi.B_NK, 16, 14336, 4096)
+    assert kid == K_SKINNY_NK and "tile=16x32" in desc and "mb=1" in desc, desc
+    # more than 16 rows of A: 64-row strips while they still give >= 192 workgroups
     kid, desc = cabi.plan(cabi.BF16, cabi.B_NK, 64, 14336, 4096)
-    assert kid == K_SKINNY_NK and "tile=64x32" in desc and "mb=4" in desc, desc
+    assert kid == K_SKINNY_NK and "tile=64x64" in desc and "mb=4" in desc and "grid=1x224x1" in desc, desc
+    kid, desc = cabi.plan(cabi.F16, cabi.B_NK, 32, 8192, 8192)
+    assert kid == K_SKINNY_NK and "tile=32x32" in desc, desc      # 128 strips of 64: too few
 
 
 def test_unaligned_16bit_operands_padded_in_the_workspace():
