@@ -40,9 +40,19 @@ template <typename T, int SW, bool NT>
 hipError_t launch_nk(int mb, const GemmParams& p, dim3 grid, hipStream_t s) {
   const dim3 block(256);
   // 1 KiB of each W row per stage for one 16-row block of A, 512 bytes otherwise; 64-row
-  // strips: 512 bytes for one or two blocks, 256 for three or four (the ring keeps >= 3 stages)
+  // strips: 512 bytes for one or two blocks, 256 for three or four (the ring keeps >= 3
+  // stages).  32-row strips with one block (more than 256 of them): 512-byte stages in a
+  // ring of 3 (72 KiB), so that two workgroups share a CU and all strips run at once
+  // instead of in 1.75 rounds (MI355X, x[1, 4096] W[14336, 4096]^T 21.4 -> 19.7 us,
+  // x[16, 4096] 23.3 -> 21.4 us, x[1, 8192] W[28672, 8192]^T 76.1 -> 73.3 us; with 16-row
+  // strips, one per CU, the deep ring is faster: x[1, 14336] W[4096, 14336]^T 20.5 vs 26.0).
   switch (mb) {
-    case 1: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 1, SW, SW == 64 ? 256 : 512, NT>), grid, block, 0, s, p); break;
+    case 1:
+      if constexpr (SW == 32)
+        hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 1, 32, 256, NT, 3>), grid, block, 0, s, p);
+      else
+        hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 1, SW, SW == 64 ? 256 : 512, NT>), grid, block, 0, s, p);
+      break;
     case 2: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 2, SW, 256, NT>), grid, block, 0, s, p); break;
     case 3: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 3, SW, SW == 64 ? 128 : 256, NT>), grid, block, 0, s, p); break;
     case 4: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, SW, SW == 64 ? 128 : 256, NT>), grid, block, 0, s, p); break;

@@ -196,14 +196,16 @@ __global__ void __launch_bounds__(256) gemm_skinny_narrow_kernel(const GemmParam
 // and read with ds_read_b128 straight into the MFMA's first operand.  As above,
 // the stage's 32-deep k-blocks are split over the 4 waves and the partial sums
 // reduced in LDS at the end; no workspace, no second launch.
-template <int MB, int SW, int KS_>
+// NSMAX caps the ring depth (otherwise as many stages as fit, up to 8), e.g. so that two
+// workgroups share a CU.
+template <int MB, int SW, int KS_, int NSMAX = 8>
 struct SkinnyNKShape {
   static constexpr int KS = KS_;
   static constexpr int PITCH = KS * 2;             // bytes per LDS row (W and A alike)
   static constexpr int W_BYTES = SW * PITCH;
   static constexpr int A_BYTES = MB * 16 * PITCH;
   static constexpr int STAGE = W_BYTES + A_BYTES;
-  static constexpr int NS = (160 * 1024) / STAGE > 8 ? 8 : (160 * 1024) / STAGE;
+  static constexpr int NS = (160 * 1024) / STAGE > NSMAX ? NSMAX : (160 * 1024) / STAGE;
   static constexpr int W_DMA = W_BYTES / 4096;  // 1 KB LDS-DMA loads per wave per stage
   static constexpr int A_DMA = A_BYTES / 4096;
   static constexpr int DMA = W_DMA + A_DMA;
@@ -215,9 +217,9 @@ struct SkinnyNKShape {
 
 // NT: stream W with the non-temporal policy (W larger than the Infinity Cache would keep
 // for the next call).
-template <typename T, int MB, int SW, int KS, bool NT = false>
+template <typename T, int MB, int SW, int KS, bool NT = false, int NSMAX = 8>
 __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p) {
-  using S = SkinnyNKShape<MB, SW, KS>;
+  using S = SkinnyNKShape<MB, SW, KS, NSMAX>;
   constexpr int NS = S::NS;
   constexpr int NB = SW / 16;  // 16-column blocks per strip
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * S::STAGE];
