@@ -71,6 +71,8 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
       return launch_skinny((DType)dtype, plan.mb, p, grid, s);
     case kSkinnyNK:
       return launch_skinny_nk((DType)dtype, plan.mb, plan.bn, p, grid, s);
+    case kTall:
+      return launch_tall((DType)dtype, lay, plan.mb, plan.bm, p, grid, s);
     case kF32Tile128:
     case kF32Tile64:
     case kF32Tile96x64:

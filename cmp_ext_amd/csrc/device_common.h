@@ -233,6 +233,39 @@ __device__ __forceinline__ void dma128_geom(int slot, int lane, int& row, int& c
   chunk = (bg & 7) ^ (pp & 7);
 }
 
+// [k][n] layout of an N-contiguous B tile: rows of `pitch` bytes (a multiple
+// of 256), 64-byte segments XORed with k%4 and their 32-byte halves with
+// (k/8)%2.  A transposing fragment read (lanes of group G at rows 8G + 0..3,
+// 8 bytes each) then covers all 64 banks once per 32 lanes; without the half
+// swap, groups G and G+1 hit the same 32 banks (measured: 8.5M bank-conflict
+// cycles per 4096^3 launch, now 0).
+__device__ __forceinline__ uint32_t kn_off(int k, int pitch, int byte_col) {
+  return (uint32_t)(k * pitch + (((byte_col >> 6) ^ (k & 3)) << 6) + ((byte_col & 63) ^ (((k >> 3) & 1) << 5)));
+}
+// Lane `lane` of 1 KB LDS-DMA load `slot` fetches row k, columns n..n+7 (the
+// inverse of kn_off at byte slot*1024 + 16*lane).
+__device__ __forceinline__ void dma_kn_geom(int slot, int lane, int pitch, int& k, int& n) {
+  const int pos = slot * 1024 + 16 * lane;
+  k = pos / pitch;
+  const int within = pos - k * pitch;
+  const int seg = (within >> 6) ^ (k & 3);
+  n = (seg * 64 + ((within & 63) ^ (((k >> 3) & 1) << 5))) >> 1;
+}
+
+// The same for rows of 128 bytes (64 columns): 32-byte slots XORed with (k/2)%2 +
+// 2((k/8)%2), so that the rows k..k+3 (4 | k) of a transposing read by 16 lanes and the
+// rows k+8..k+11 of the next 16 lanes fill the 64 banks once.
+__device__ __forceinline__ int kn128_swz(int k) { return ((k >> 1) & 1) | (((k >> 3) & 1) << 1); }
+__device__ __forceinline__ uint32_t kn128_off(int k, int byte_col) {
+  return (uint32_t)(k * 128 + (((byte_col >> 5) ^ kn128_swz(k)) << 5) + (byte_col & 31));
+}
+__device__ __forceinline__ void dma_kn128_geom(int slot, int lane, int& k, int& n) {
+  const int pos = slot * 1024 + 16 * lane;
+  k = pos >> 7;
+  const int within = pos & 127;
+  n = ((((within >> 5) ^ kn128_swz(k)) << 5) + (within & 31)) >> 1;
+}
+
 // ---------------------------------------------------------------------------
 // Tile order.  The dispatcher hands workgroup w (x fastest, then z) to XCD
 // w % 8; consecutive logical tiles -- batch entry by batch entry -- are given to

@@ -46,7 +46,8 @@ enum KernelId : int {
   kF32Tile16K4 = 12,  // same with 16x64 tiles (M <= 16)
   kStream64x128 = 13, // f16/bf16, M <= 64, K <= 256, B is [K,N]: persistent workgroups stream 128-column tiles
   kStream128x128 = 14,  // same with 128-row tiles (64 < M <= 128)
-  kNumKernels = 15
+  kTall = 15,         // f16/bf16, N <= 128: strips of A's rows over all of K, B small ([N,K] or [K,N])
+  kNumKernels = 16
 };
 
 }  // namespace cmpext3

@@ -20,6 +20,8 @@ hipError_t launch_tile_bf16_nk_whole(KernelId id, const GemmParams& p, dim3 grid
 hipError_t launch_tile_bf16_nk_ragged(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s);
 hipError_t launch_skinny(DType dt, int mb, const GemmParams& p, dim3 grid, hipStream_t s);
 hipError_t launch_skinny_nk(DType dt, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s);
+// N <= 16 * mb: strips of `strip` rows of A over all of K, B as [N, K] or [K, N] (layout)
+hipError_t launch_tall(DType dt, BLayout lay, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s);
 hipError_t launch_skinny_wide(DType dt, int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid,
                               hipStream_t s);
 hipError_t launch_skinny_reduce(DType dt, const GemmParams& p, const float* ws, int splits, int batch,

@@ -113,6 +113,7 @@ const char* kernel_name(KernelId id) {
     case kF32Tile16K4: return "f32tile16x64k4";
     case kGeneric16: return "generic64x64";
     case kStream64x128: return "stream64x128";
+    case kTall: return "tall";
     case kStream128x128: return "stream128x128";
     default: return "?";
   }
@@ -121,7 +122,7 @@ const char* kernel_name(KernelId id) {
 }  // namespace
 
 namespace {
-// Tuning override: CMPEXT3_GEMM_CONFIG="kernel=<name>[,splits=<s>]" (names as in the plan
+// Tuning override: CMPEXT3_GEMM_CONFIG="kernel=<name>[,splits=<s>][,strip=<rows>]" (names as in the plan
 // strings, e.g. tile128x128, stream64x128, generic64x64, f32tile96x64) replaces the
 // selector's choice wherever that kernel's own requirements hold for the call; otherwise,
 // and for an unknown name or malformed value, it is ignored.  Read on every plan, so a
@@ -130,6 +131,7 @@ namespace {
 struct Override {
   int kernel = -1;
   int splits = 1;
+  int strip = 0;  // tall: rows of A per workgroup (32 or 64; 0: the selector's)
 };
 
 Override read_override() {
@@ -146,6 +148,9 @@ Override read_override() {
     } else if (strncmp(tok, "splits=", 7) == 0) {
       const int v = atoi(tok + 7);
       if (v >= 1 && v <= 16) o.splits = v;
+    } else if (strncmp(tok, "strip=", 6) == 0) {
+      const int v = atoi(tok + 6);
+      if (v == 32 || v == 64) o.strip = v;
     }
   }
   return o;
@@ -161,9 +166,24 @@ int forced_splits(const Request& r, int s, int64_t* ksplit) {
   return s;
 }
 
+// The tall kernel for N <= 128 (16-row blocks of B's columns: 4 up to 64 columns, else 8)
+// with strips of `strip` rows of A.
+Plan tall_plan(const Request& r, int strip, int group_m) {
+  Plan q{};
+  q.kernel = kTall;
+  q.group_m = group_m;
+  q.threads = 256;
+  q.splits = 1;
+  q.mb = r.N <= 64 ? 4 : 8;
+  q.bm = strip;
+  q.bn = 16 * q.mb;
+  return q;
+}
+
 // Applies the override to a 16-bit plan: a tiled kernel (optionally split) when `fast`,
-// the streaming kernel when `stream_ok`, the generic kernel always.
-void override16(const Request& r, bool fast, bool stream_ok, Plan* p) {
+// the streaming kernel when `stream_ok`, the tall kernel when `tall_ok`, the generic
+// kernel always.
+void override16(const Request& r, bool fast, bool stream_ok, bool tall_ok, Plan* p) {
   const Override o = read_override();
   if (o.kernel < 0) return;
   Plan q{};
@@ -200,6 +220,10 @@ void override16(const Request& r, bool fast, bool stream_ok, Plan* p) {
       q.bm = 64;
       q.bn = 64;
       q.forced = true;  // no padded copies in its place
+      break;
+    case kTall:
+      if (!tall_ok) return;
+      q = tall_plan(r, o.strip ? o.strip : 64, p->group_m);
       break;
     default:
       return;
@@ -307,6 +331,13 @@ int make_plan_core(const Request& r, Plan* plan) {
                            r.ldc % 8 == 0 && (!batched || (r.stride_a == 0 && r.stride_c % 8 == 0)) &&
                            (!r.has_bias || r.bias_row) && 128 * r.ldb * 2 <= kIntMax &&
                            128 * r.ldc * 2 <= kIntMax && cdiv(r.N, 128) * r.batch <= kIntMax;
+    // what the tall kernel needs: A and B as for `fast` (C is written element by element, so
+    // its alignment does not matter) and a narrow B, as [N, K] or as [K, N] in 16-byte
+    // column chunks
+    const bool tall_ok = (r.align_a ? r.align_a : r.align) >= 16 && (r.align_b ? r.align_b : r.align) >= 16 &&
+                         r.K % 8 == 0 && r.lda % 8 == 0 && r.ldb % 8 == 0 && r.N <= 128 &&
+                         (r.layout == kNK || r.N % 8 == 0) &&
+                         (!batched || (r.stride_a % 8 == 0 && r.stride_b % 8 == 0));
     if (skinny_ok && !skinny_tiles_enough && r.layout == kNK) {
       // B is [N, K] (a Linear weight): strips of W rows over all of K; 16-row
       // strips when 32-row ones would leave CUs idle.  With more than 16 rows of A every
@@ -358,6 +389,17 @@ int make_plan_core(const Request& r, Plan* plan) {
       p.bm = r.M <= 64 ? 64 : 128;
       p.bn = 128;
       p.threads = r.M <= 64 ? 256 : 512;
+    } else if (tall_ok && r.N <= 64 && r.M >= 1024 && r.K >= 1024 && cdiv(r.M, 128) * r.batch < kNumCUs &&
+               (r.K <= 2048 || (r.K <= 4096 && r.M * r.batch >= 8192))) {
+      // A narrow B (<= 64 columns) under fewer 128-row tiles than CUs: the tile kernels would
+      // split K (or leave CUs idle) to fill the GPU; strips of A's rows over all of K stream
+      // A once instead (MI355X, fp16, best strip vs the selector's tile128x128 (+ split):
+      // 2048 x 64 x 2048 8.5 vs 10.8 us, 8192 x 64 x 2048 10.4 vs 16.1, 16384 x 64 x 2048
+      // 16.6 vs 25.0, 16384 x 16 x 4096 27.7 vs 30.7, attention's P V over 8 x 2048 x 2048
+      // with 64 columns 18.8 vs 25.7; measured slower from K = 8192, with 64 < N <= 128, or
+      // at K = 4096 below 8192 rows).  64-row strips once they give every CU one and K >=
+      // 2048, else 32-row strips two workgroups per CU.
+      p = tall_plan(r, cdiv(r.M, 64) * r.batch >= kNumCUs && r.K >= 2048 ? 64 : 32, p.group_m);
     } else if (fast && r.M <= 64 && r.K <= 1024 && cdiv(r.N, 256) * r.batch >= kNumCUs) {
       // Short-K products with few rows and many columns are HBM-bound; 64-row tiles
       // waste no MFMA rows and keep more loads in flight per CU (MI355X, 64x256 vs
@@ -401,7 +443,7 @@ int make_plan_core(const Request& r, Plan* plan) {
       p.bm = 64;
       p.bn = 64;
     }
-    override16(r, fast, stream_ok, &p);
+    override16(r, fast, stream_ok, tall_ok, &p);
   }
   if (p.splits == 0) p.splits = 1;
   if (p.kernel == kSkinny || p.kernel == kSkinnyWide || p.kernel == kSkinnyNK || p.kernel == kStream64x128 ||
@@ -547,7 +589,7 @@ std::string describe(const Request& r, const Plan& p) {
            kernel_name(p.kernel), dt[r.dtype], r.layout == kKN ? "KN" : "NK", p.bm, p.bn, p.tiles_m,
            p.tiles_n, (long long)r.batch, p.threads);
   std::string s(buf);
-  if (p.kernel == kSkinny || p.kernel == kSkinnyWide || p.kernel == kSkinnyNK) {
+  if (p.kernel == kSkinny || p.kernel == kSkinnyWide || p.kernel == kSkinnyNK || p.kernel == kTall) {
     snprintf(buf, sizeof buf, " mb=%d", p.mb);
     s += buf;
   }

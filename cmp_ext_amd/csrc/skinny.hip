@@ -25,17 +25,6 @@ hipError_t launch(int mb, const GemmParams& p, dim3 grid, hipStream_t s) {
 }  // namespace
 
 namespace {
-// The streamed operand (B, or W) of one launch is read with the non-temporal policy when it
-// is at least kStreamOnceBytes: a smaller one may still sit in the 256 MB Infinity Cache at
-// the next call, which the policy would give up (MI355X, fp16, operands rotating over four
-// buffers: 16 x 8192 x 8192 27.6 -> 26.1 us, W of 8192 x 8192 for one row 28.3 -> 25.0 us,
-// 14336 x 4096 for 16 rows 25.9 -> 23.3 us; 4096 x 4096, whose four copies fit the cache,
-// 7.9 -> 8.8 us).
-constexpr int64_t kStreamOnceBytes = 64ll << 20;
-bool stream_once(int64_t rows, int64_t cols, int64_t stride, unsigned batch) {
-  return rows * cols * 2 * (stride != 0 ? (int64_t)batch : 1) >= kStreamOnceBytes;
-}
-
 template <typename T, int SW, bool NT>
 hipError_t launch_nk(int mb, const GemmParams& p, dim3 grid, hipStream_t s) {
   const dim3 block(256);

@@ -43,6 +43,17 @@ struct SkinnyShape {
   static_assert(4 * MB * 16 * kSkinnyStrip * 4 <= NS * STAGE, "reduction fits the ring");
 };
 
+// The streamed operand (B, W, or A for the swapped kernel) of one launch is read with the non-temporal policy when it
+// is at least kStreamOnceBytes: a smaller one may still sit in the 256 MB Infinity Cache at
+// the next call, which the policy would give up (MI355X, fp16, operands rotating over four
+// buffers: 16 x 8192 x 8192 27.6 -> 26.1 us, W of 8192 x 8192 for one row 28.3 -> 25.0 us,
+// 14336 x 4096 for 16 rows 25.9 -> 23.3 us; 4096 x 4096, whose four copies fit the cache,
+// 7.9 -> 8.8 us).
+constexpr int64_t kStreamOnceBytes = 64ll << 20;
+inline bool stream_once(int64_t rows, int64_t cols, int64_t stride, unsigned batch) {
+  return rows * cols * 2 * (stride != 0 ? (int64_t)batch : 1) >= kStreamOnceBytes;
+}
+
 __device__ __forceinline__ int strip_order(int wg, int total) {
   const int xcd = wg & 7, local = wg >> 3;
   const int base = total >> 3, rem = total & 7;
@@ -198,30 +209,42 @@ __global__ void __launch_bounds__(256) gemm_skinny_narrow_kernel(const GemmParam
 // reduced in LDS at the end; no workspace, no second launch.
 // NSMAX caps the ring depth (otherwise as many stages as fit, up to 8), e.g. so that two
 // workgroups share a CU.
-template <int MB, int SW, int KS_, int NSMAX = 8>
+//
+// SWAP: the same kernel for the mirror case, N <= 16*MB and M large (C = A B with a
+// narrow B, e.g. attention's P V, or x W^T with few rows of W, e.g. a router): the
+// streamed rows are A's (strips of SW rows of C), the small operand is B -- as [N, K]
+// (XKN false: read like A above) or as [K, N] (XKN true: stored [k][n] in rows of 32*MB
+// bytes, kn128_off / kn_off, and read with the transposing ds_read_b64_tr_b16) -- and C
+// is written transposed from the reduction.
+template <int MB, int SW, int KS_, int NSMAX = 8, bool SWAP = false>
 struct SkinnyNKShape {
   static constexpr int KS = KS_;
   static constexpr int PITCH = KS * 2;             // bytes per LDS row (W and A alike)
   static constexpr int W_BYTES = SW * PITCH;
-  static constexpr int A_BYTES = MB * 16 * PITCH;
+  static constexpr int A_BYTES = MB * 16 * PITCH;  // = KS rows of 32*MB bytes ([k][n] form)
   static constexpr int STAGE = W_BYTES + A_BYTES;
   static constexpr int NS = (160 * 1024) / STAGE > NSMAX ? NSMAX : (160 * 1024) / STAGE;
   static constexpr int W_DMA = W_BYTES / 4096;  // 1 KB LDS-DMA loads per wave per stage
   static constexpr int A_DMA = A_BYTES / 4096;
   static constexpr int DMA = W_DMA + A_DMA;
   static constexpr int KB = KS / 32 / 4;        // 32-deep k-blocks per wave per stage
+  // reduction rows (floats): MB*16 x rows of SW, or (SWAP) SW rows of MB*16 + 4 (the pad
+  // spreads the four lane groups' writes over the banks)
+  static constexpr int RED = SWAP ? SW * (MB * 16 + 4) : MB * 16 * SW;
   static_assert(W_BYTES % 4096 == 0 && A_BYTES % 4096 == 0 && KB >= 1, "whole DMA loads per wave");
   static_assert(NS >= 3 && (NS - 2) * DMA <= 63, "ring depth / vmcnt range");
-  static_assert(4 * MB * 16 * SW * 4 <= NS * STAGE, "reduction fits the ring");
+  static_assert(4 * RED * 4 <= NS * STAGE, "reduction fits the ring");
 };
 
 // NT: stream W with the non-temporal policy (W larger than the Infinity Cache would keep
 // for the next call).
-template <typename T, int MB, int SW, int KS, bool NT = false, int NSMAX = 8>
+template <typename T, int MB, int SW, int KS, bool NT = false, int NSMAX = 8, bool SWAP = false, bool XKN = false>
 __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p) {
-  using S = SkinnyNKShape<MB, SW, KS, NSMAX>;
+  using S = SkinnyNKShape<MB, SW, KS, NSMAX, SWAP>;
   constexpr int NS = S::NS;
   constexpr int NB = SW / 16;  // 16-column blocks per strip
+  constexpr int XP = 32 * MB;  // bytes per k row of a [K, N] small operand in LDS
+  static_assert(!XKN || (SWAP && (XP == 128 || XP == 256)), "[K, N] small operand: swapped roles, 64 or 128 columns");
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * S::STAGE];
 
   const int tid = threadIdx.x;
@@ -229,11 +252,14 @@ __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int strip = strip_order(blockIdx.x, gridDim.x);
   const int n0 = strip * SW;
-  const int M = p.M, N = p.N, K = p.K;
+  const int K = p.K;
+  // W: the streamed operand (B's rows, or A's when SWAP); X: the small one (A, or B)
+  const int w_rows = SWAP ? p.M : p.N, x_rows = SWAP ? p.N : p.M;
   const int64_t bz = blockIdx.z;
-  const int64_t lda = p.lda, ldb = p.ldb;
-  const T* Ab = (const T*)p.A + bz * p.stride_a;
-  const T* Wb = (const T*)p.B + bz * p.stride_b + (int64_t)n0 * ldb;
+  const int64_t ldw = SWAP ? p.lda : p.ldb, ldx = SWAP ? p.ldb : p.lda;
+  const T* Wb = SWAP ? (const T*)p.A + bz * p.stride_a + (int64_t)n0 * ldw
+                     : (const T*)p.B + bz * p.stride_b + (int64_t)n0 * ldw;
+  const T* Xb = SWAP ? (const T*)p.B + bz * p.stride_b : (const T*)p.A + bz * p.stride_a;
 
   // ---- DMA sources: rows of PITCH bytes, chunk c of row r stored at chunk c ^ (r % 16) ----
   auto geom = [&](int piece, int& row, int& chunk) {
@@ -247,24 +273,34 @@ __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p)
   for (int i = 0; i < S::W_DMA; ++i) {
     int row, chunk;
     geom(wave * S::W_DMA + i, row, chunk);
-    w_off[i] = (n0 + row < N) ? (uint32_t)(row * ldb + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
+    w_off[i] = (n0 + row < w_rows) ? (uint32_t)(row * ldw + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
     w_k[i] = 8 * chunk;
   }
   uint32_t a_off[S::A_DMA];
   int a_k[S::A_DMA];
 #pragma unroll
   for (int i = 0; i < S::A_DMA; ++i) {
-    int row, chunk;
-    geom(wave * S::A_DMA + i, row, chunk);
-    a_off[i] = (row < M) ? (uint32_t)(row * lda + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
-    a_k[i] = 8 * chunk;
+    if constexpr (XKN) {  // row k of the stage, columns n .. n+7
+      int k, n;
+      if constexpr (XP == 128)
+        dma_kn128_geom(wave * S::A_DMA + i, lane, k, n);
+      else
+        dma_kn_geom(wave * S::A_DMA + i, lane, XP, k, n);
+      a_off[i] = (n < x_rows) ? (uint32_t)(k * ldx + n) * (uint32_t)sizeof(T) : kBufOOB;
+      a_k[i] = k;
+    } else {
+      int row, chunk;
+      geom(wave * S::A_DMA + i, row, chunk);
+      a_off[i] = (row < x_rows) ? (uint32_t)(row * ldx + 8 * chunk) * (uint32_t)sizeof(T) : kBufOOB;
+      a_k[i] = 8 * chunk;
+    }
   }
   auto load_stage = [&](int st) {
     const int k0 = st * S::KS;
     const uint32_t dst = lds_addr(smem) + (uint32_t)((st % NS) * S::STAGE);
     const int krem = K - k0;
     const i32x4 rw = make_rsrc_sgpr(Wb + k0);
-    const i32x4 ra = make_rsrc_sgpr(Ab + k0);
+    const i32x4 ra = make_rsrc_sgpr(XKN ? Xb + (int64_t)k0 * ldx : Xb + k0);
 #pragma unroll
     for (int i = 0; i < S::W_DMA; ++i)
       if constexpr (NT)
@@ -277,9 +313,10 @@ __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p)
   };
 
   // ---- fragments: lane (c = l%16, g = l/16) ----
-  // first MFMA operand: W row 16h + c (column n0 + 16h + c of C) at k = kb + 8g .. +7
-  // second operand:     A row 16mb + c at the same k
+  // first MFMA operand: W row 16h + c at k = kb + 8g .. +7
+  // second operand:     X row 16mb + c at the same k
   const int c = lane & 15, g = lane >> 4;
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
   f32x4 acc[NB][MB];
 #pragma unroll
   for (int h = 0; h < NB; ++h)
@@ -293,8 +330,23 @@ __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p)
       const int kc = (wave * S::KB + b) * 4 + g;  // 16-byte chunk of the lane's 8 k
       u32x4 af[MB];
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-        af[mb] = *(const u32x4*)(stage + S::W_BYTES + (16 * mb + c) * S::PITCH + 16 * (kc ^ c));
+      for (int mb = 0; mb < MB; ++mb) {
+        if constexpr (XKN) {
+          // rows 8kc + 4r + c/4, columns 16mb + 4(c%4) .. +3: the transposing read hands
+          // lane c column 16mb + c at the four k
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const int k = 8 * kc + 4 * r + (c >> 2), bc = 32 * mb + 8 * (c & 3);
+            const unsigned char* q = stage + S::W_BYTES + (XP == 128 ? kn128_off(k, bc) : kn_off(k, XP, bc));
+            const u32x2 v = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)q));
+            af[mb][2 * r] = v.x;
+            af[mb][2 * r + 1] = v.y;
+          }
+        } else {
+          af[mb] = *(const u32x4*)(stage + S::W_BYTES + (16 * mb + c) * S::PITCH + 16 * (kc ^ c));
+        }
+      }
 #pragma unroll
       for (int h = 0; h < NB; ++h) {
         const u32x4 wf = *(const u32x4*)(stage + (16 * h + c) * S::PITCH + 16 * (kc ^ c));
@@ -316,26 +368,49 @@ __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p)
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" : : : "memory");
 
   // ---- reduce the 4 waves' partial sums through LDS (the ring is free) ----
-  // acc[h][mb][r] = C[16*mb + c][n0 + 16*h + 4*g + r]
-  float* red = (float*)smem;  // [wave][MB*16][SW]
-#pragma unroll
-  for (int h = 0; h < NB; ++h)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[(wave * MB * 16 + 16 * mb + c) * SW + 16 * h + 4 * g + r] = acc[h][mb][r];
-  __syncthreads();
+  // acc[h][mb][r] = (X row 16*mb + c) . (W row n0 + 16*h + 4*g + r)
+  float* red = (float*)smem;
   T* Cb = (T*)p.C + bz * p.stride_c;
   const uint16_t* bias = (const uint16_t*)p.bias;
-  for (int o = tid; o < MB * 16 * SW; o += 256) {
-    const int row = o / SW, col = o % SW;
-    const int n = n0 + col;
-    if (row >= M || n >= N) continue;
-    float s = 0.f;
+  if constexpr (SWAP) {
+    // red[wave][W row][X row], rows of RP floats; C[n0 + W row][X row]
+    constexpr int XR = MB * 16, RP = MB * 16 + 4;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) s += red[(w * MB * 16 + row) * SW + col];
-    if (bias) s += from_bits<T>(bias[p.bias_row ? row : n]);
-    ((uint16_t*)(Cb + (int64_t)row * p.ldc))[n] = to_bits<T>(s);
+    for (int h = 0; h < NB; ++h)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(wave * SW + 16 * h + 4 * g + r) * RP + 16 * mb + c] = acc[h][mb][r];
+    __syncthreads();
+    for (int o = tid; o < SW * XR; o += 256) {
+      const int wr = o / XR, xr = o % XR;
+      const int m = n0 + wr;
+      if (m >= w_rows || xr >= x_rows) continue;
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) s += red[(w * SW + wr) * RP + xr];
+      if (bias) s += from_bits<T>(bias[p.bias_row ? m : xr]);
+      ((uint16_t*)(Cb + (int64_t)m * p.ldc))[xr] = to_bits<T>(s);
+    }
+  } else {
+    // red[wave][X row][SW]; C[X row][n0 + column]
+#pragma unroll
+    for (int h = 0; h < NB; ++h)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(wave * MB * 16 + 16 * mb + c) * SW + 16 * h + 4 * g + r] = acc[h][mb][r];
+    __syncthreads();
+    for (int o = tid; o < MB * 16 * SW; o += 256) {
+      const int row = o / SW, col = o % SW;
+      const int n = n0 + col;
+      if (row >= x_rows || n >= w_rows) continue;
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) s += red[(w * MB * 16 + row) * SW + col];
+      if (bias) s += from_bits<T>(bias[p.bias_row ? row : n]);
+      ((uint16_t*)(Cb + (int64_t)row * p.ldc))[n] = to_bits<T>(s);
+    }
   }
 }
 

@@ -1,0 +1,44 @@
+// Instantiations of the strips-of-W kernel with swapped roles (gemm_skinny_nk_kernel,
+// SWAP): C = A B (+ bias) with N <= 128 and many rows of A, which stream through the
+// workgroups in strips while the small B is re-read from L2 by each of them.
+#include <stdint.h>
+
+#include "kernels.h"
+#include "skinny_kernel.h"
+
+namespace cmpext3 {
+namespace {
+// KS = 128 k per stage: strip rows of 256 bytes, B k-rows of 64 or 128 columns.  32-row
+// strips with B of 64 columns run in a ring of three 24 KiB stages, two workgroups per CU.
+template <typename T, bool XKN, bool NT>
+hipError_t launch_tall_t(int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {
+  const dim3 block(256);
+  if (mb == 4 && strip == 32)
+    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, 32, 128, NT, 3, true, XKN>), grid, block, 0, s, p);
+  else if (mb == 4 && strip == 64)
+    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, 64, 128, NT, 8, true, XKN>), grid, block, 0, s, p);
+  else if (mb == 8 && strip == 32)
+    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 8, 32, 128, NT, 8, true, XKN>), grid, block, 0, s, p);
+  else if (mb == 8 && strip == 64)
+    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 8, 64, 128, NT, 8, true, XKN>), grid, block, 0, s, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+template <typename T>
+hipError_t launch_tall_t(BLayout lay, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {
+  const bool nt = stream_once(p.M, p.K, p.stride_a, grid.z);
+  if (lay == kKN) return nt ? launch_tall_t<T, true, true>(mb, strip, p, grid, s) : launch_tall_t<T, true, false>(mb, strip, p, grid, s);
+  return nt ? launch_tall_t<T, false, true>(mb, strip, p, grid, s) : launch_tall_t<T, false, false>(mb, strip, p, grid, s);
+}
+}  // namespace
+
+hipError_t launch_tall(DType dt, BLayout lay, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {
+  // every column of C in the workgroup's block, one workgroup per strip of A's rows
+  if (p.N > 16 * mb || grid.y != 1 || (int64_t)grid.x * strip < p.M) return hipErrorInvalidValue;
+  if (dt == kF16) return launch_tall_t<_Float16>(lay, mb, strip, p, grid, s);
+  if (dt == kBF16) return launch_tall_t<__bf16>(lay, mb, strip, p, grid, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace cmpext3

@@ -57,25 +57,6 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// [k][n] layout of an N-contiguous B tile: rows of `pitch` bytes (a multiple
-// of 256), 64-byte segments XORed with k%4 and their 32-byte halves with
-// (k/8)%2.  A transposing fragment read (lanes of group G at rows 8G + 0..3,
-// 8 bytes each) then covers all 64 banks once per 32 lanes; without the half
-// swap, groups G and G+1 hit the same 32 banks (measured: 8.5M bank-conflict
-// cycles per 4096^3 launch, now 0).
-__device__ __forceinline__ uint32_t kn_off(int k, int pitch, int byte_col) {
-  return (uint32_t)(k * pitch + (((byte_col >> 6) ^ (k & 3)) << 6) + ((byte_col & 63) ^ (((k >> 3) & 1) << 5)));
-}
-// Lane `lane` of 1 KB LDS-DMA load `slot` fetches row k, columns n..n+7 (the
-// inverse of kn_off at byte slot*1024 + 16*lane).
-__device__ __forceinline__ void dma_kn_geom(int slot, int lane, int pitch, int& k, int& n) {
-  const int pos = slot * 1024 + 16 * lane;
-  k = pos / pitch;
-  const int within = pos - k * pitch;
-  const int seg = (within >> 6) ^ (k & 3);
-  n = (seg * 64 + ((within & 63) ^ (((k >> 3) & 1) << 5))) >> 1;
-}
-
 template <int BM, int BN, bool KN, int WM, int WN>
 struct Tile16Shape {
   static constexpr int BK = 64;

@@ -20,6 +20,7 @@ TAIL = 64  # elements after every buffer's last logical element
 N_CASES = 320
 N_STREAM = 6
 N_WIDE = 3
+N_TALL = 6
 
 
 def _round8(x):
@@ -94,11 +95,32 @@ def draw_wide_case(rng: np.random.Generator, idx: int) -> dict:
                 sample=sorted({0, batch // 2, batch - 1}))
 
 
+def draw_tall_case(rng: np.random.Generator, idx: int) -> dict:
+    """Many rows of A, a narrow B (<= 64 columns) and K of 1024 .. 2048: strips of A's rows
+    (the tall kernel).  Padded pitches, offset bases and batch gaps in multiples of 8."""
+    dtype = ["fp16", "bf16"][rng.integers(2)]
+    layout = [cabi.B_KN, cabi.B_NK][rng.integers(2)]
+    M = int(rng.integers(1024, 3001))
+    N = int(rng.choice([8, 16, 40, 64])) if layout == cabi.B_KN else int(rng.integers(1, 65))
+    K = int(rng.choice([1024, 1032, 1536, 2048]))
+    batch = int(rng.choice([1, 2]))
+    lda = K + int(rng.choice([0, 8]))
+    ldb = (N if layout == cabi.B_KN else K) + int(rng.choice([0, 8]))
+    ldc = N + int(rng.choice([0, 3, 8]))
+    rows_b = K if layout == cabi.B_KN else N
+    return dict(idx=idx, dtype=dtype, layout=layout, M=M, N=N, K=K, lda=lda, ldb=ldb, ldc=ldc,
+                off_a=int(rng.choice([0, 8])), off_b=int(rng.choice([0, 8])), off_c=int(rng.choice([0, 1])),
+                batch=batch, stride_a=M * lda + int(rng.choice([0, 8])), stride_b=rows_b * ldb + int(rng.choice([0, 8])),
+                stride_c=M * ldc + int(rng.choice([0, 5])), bias=[None, "col", "row"][rng.integers(3)],
+                off_bias=int(rng.choice([0, 1])), workspace=bool(rng.integers(2)), sample=None)
+
+
 def cases():
     rng = np.random.default_rng(20261202)
     out = [draw_case(rng, i) for i in range(N_CASES)]
     out += [draw_stream_case(rng, N_CASES + i, i % 2 == 1) for i in range(N_STREAM)]
     out += [draw_wide_case(rng, N_CASES + N_STREAM + i) for i in range(N_WIDE)]
+    out += [draw_tall_case(rng, N_CASES + N_STREAM + N_WIDE + i) for i in range(N_TALL)]
     return out
 
 

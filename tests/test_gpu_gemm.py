@@ -26,7 +26,7 @@ MATMUL = {"fp16": cmpext3.fp16_matmul, "bf16": cmpext3.bf16_matmul, "fp32": cmpe
 KERNEL_NAMES = ["tile256x256", "tile256x224", "tile128x128", "tile64x256", "skinny", "skinny_wide", "skinny_nk",
                 "f32tile128x128",
                 "f32tile64x64", "f32tile96x64", "f32tile64x64k4", "f32tile16x64k4", "generic64x64", "stream64x128",
-                "stream128x128"]
+                "stream128x128", "tall"]
 SEEN_KERNELS = set()
 
 
@@ -337,6 +337,49 @@ def test_skinny_nk_wide_strips(dtype, M, N, K, bias):
     assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
     again = cmpext3.linear(x.cuda(), w.cuda(), None if b is None else b.cuda())
     assert torch.equal(out, again)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_tall_narrow_b_through_the_operators(dtype):
+    """A narrow B under few 128-row tiles runs on strips of A's rows (the tall kernel):
+    attention's P V through bmm (B as [K, N], 64-row strips over a batch), a router-shaped
+    Linear with a column bias (B as [N, K], 32-row strips) and a matmul with 16 columns
+    written into a column slice of a wider C; against the oracle, deterministic."""
+    g = torch.Generator().manual_seed(23)
+    dt = DT[dtype]
+    p = (torch.randn(8, 2048, 2048, generator=g) / np.sqrt(2048)).to(dt)
+    v = torch.randn(8, 2048, 64, generator=g).to(dt)
+    print(f"tall bmm {dtype} 8x2048x64x2048", flush=True)
+    out = cmpext3.bmm(p.cuda(), v.cuda())
+    name, desc = launched()
+    assert name == "tall" and "tile=64x64" in desc, desc
+    torch.cuda.synchronize()
+    ref = O.bmm_f64(O.to_f64(p), O.to_f64(v))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    assert torch.equal(out, cmpext3.bmm(p.cuda(), v.cuda()))
+
+    x = (torch.randn(3000, 1032, generator=g) / np.sqrt(1032)).to(dt)
+    w = torch.randn(40, 1032, generator=g).to(dt)
+    b = torch.randn(40, generator=g).to(dt)
+    print(f"tall linear {dtype} 3000x40x1032", flush=True)
+    out = cmpext3.linear(x.cuda(), w.cuda(), b.cuda())
+    name, desc = launched()
+    assert name == "tall" and "tile=32x64" in desc and "layout=NK" in desc, desc
+    torch.cuda.synchronize()
+    ref = O.linear_f64(O.to_f64(x), O.to_f64(w), O.to_f64(b))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+
+    a = (torch.randn(4096, 2048, generator=g) / np.sqrt(2048)).to(dt).cuda()
+    bm = torch.randn(2048, 16, generator=g).to(dt).cuda()
+    cw = torch.full((4096, 24), float("nan"), dtype=dt, device="cuda")
+    print(f"tall C ABI {dtype} 4096x16x2048 into C[:, 3:19]", flush=True)
+    st, name, desc = cabi_call(CODE[dtype], cabi.B_KN, a, 2048, 0, bm, 16, 0, cw[:, 3:19], 24, 0, None, 4096, 16, 2048)
+    assert st == cabi.OK and name == "tall", desc
+    torch.cuda.synchronize()
+    got = cw.cpu()
+    assert torch.isnan(got[:, :3].float()).all() and torch.isnan(got[:, 19:].float()).all()
+    ref = O.matmul_f64(O.to_f64(a.cpu()), O.to_f64(bm.cpu()))
+    assert O.rel_frobenius(O.to_f64(got[:, 3:19]), ref) <= O.TOLERANCE[dtype]
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])

@@ -5,7 +5,8 @@ which this file checks for parity: the streaming kernel with only one to a few
 128-column tiles per workgroup (its ring filling and draining within a tile or two,
 chunks past the end loaded through empty descriptors), over one or several row
 blocks, with one or two K chunks; the 256x256 tile with a K split and a batch; the
-generic kernel on aligned operands; an fp32 tile with a K split.
+generic kernel on aligned operands; an fp32 tile with a K split; the tall kernel (strips
+of A's rows, B of at most 128 columns as [K, N] or [N, K]) with both strip heights.
 """
 import pytest
 import torch
@@ -25,17 +26,22 @@ def _gpu():
         pytest.skip("no GPU")
 
 
-def _run(dtype, M, N, K, batch, shared_a, bias, workspace, seed):
+def _run(dtype, M, N, K, batch, shared_a, bias, workspace, seed, nk=False, ldc=None):
     """C[b] = A[b] B[b] (+ bias per row if bias == "row", per column if "col") through a
-    prepared call; returns (kernel description, max relative error over the batch)."""
+    prepared call, B given as [K, N] (or [N, K] if nk), C rows `ldc` apart (default N);
+    returns (kernel description, max relative error over the batch)."""
     g = torch.Generator().manual_seed(seed)
     dt = DT[dtype]
+    ldc = ldc or N
     a = (torch.randn(1 if shared_a else batch, M, K, generator=g) / max(K, 1) ** 0.5).to(dt)
     b = torch.randn(batch, K, N, generator=g).to(dt)
     bv = torch.randn(M if bias == "row" else N, generator=g).to(dt) if bias else None
-    c = torch.full((batch, M, N), float("nan"), dtype=dt, device="cuda")
-    ag, bg = a.cuda(), b.cuda()
-    st, call = cabi.prepare(CODE[dtype], cabi.B_KN, ag, K, 0 if shared_a else M * K, bg, N, K * N, c, N, M * N,
+    cfull = torch.full((batch, M, ldc), float("nan"), dtype=dt, device="cuda")
+    c = cfull[:, :, :N]
+    ag = a.cuda()
+    bg = b.transpose(1, 2).contiguous().cuda() if nk else b.cuda()
+    st, call = cabi.prepare(CODE[dtype], cabi.B_NK if nk else cabi.B_KN, ag, K, 0 if shared_a else M * K,
+                            bg, K if nk else N, K * N, c, ldc, M * ldc,
                             None if bv is None else bv.cuda(), M, N, K, batch,
                             cabi.BIAS_PER_ROW if bias == "row" else 0, (1 << 40) if workspace else 0)
     assert st == cabi.OK
@@ -47,6 +53,8 @@ def _run(dtype, M, N, K, batch, shared_a, bias, workspace, seed):
     torch.cuda.synchronize()
     out = c.cpu()
     err = 0.0
+    if ldc > N:  # the columns past N are untouched
+        assert torch.isnan(cfull[:, :, N:].float()).all()
     for i in range(batch):
         r = O.matmul_f64(O.to_f64(a[0 if shared_a else i]), O.to_f64(b[i]))
         if bias == "row":
@@ -93,3 +101,20 @@ def test_forced_fp32_tile_split(monkeypatch):
     desc, err = _run("fp32", 300, 260, 2100, 1, False, "col", True, 9)
     assert desc.startswith("kernel=f32tile128x128") and "splits=4" in desc, desc
     assert err <= O.TOLERANCE["fp32"], err
+
+
+@pytest.mark.parametrize("dtype,M,N,K,batch,bias,nk,strip,ldc", [
+    ("fp16", 2048, 64, 2048, 2, None, False, 64, None),    # B as [K, N], 64 columns, whole stages
+    ("bf16", 1000, 64, 200, 3, "col", False, 32, None),    # ragged strips and last stage
+    ("fp16", 300, 8, 136, 1, "row", False, 64, 24),        # one column block, C rows 24 apart
+    ("fp16", 777, 72, 264, 2, "col", False, 64, None),     # 72 columns: the 128-column form
+    ("bf16", 513, 128, 1032, 1, "row", False, 32, 136),    # 128 columns, 32-row strips
+    ("fp16", 2048, 64, 2048, 2, "col", True, 64, None),    # B as [N, K] (a router's weight)
+    ("bf16", 1000, 40, 72, 2, None, True, 32, None),       # [N, K], 40 rows, short K
+    ("fp16", 129, 128, 520, 3, "row", True, 64, 130),      # [N, K], 128 rows, odd C pitch
+])
+def test_forced_tall(monkeypatch, dtype, M, N, K, batch, bias, nk, strip, ldc):
+    monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", f"kernel=tall,strip={strip}")
+    desc, err = _run(dtype, M, N, K, batch, False, bias, False, M + N + K, nk=nk, ldc=ldc)
+    assert desc.startswith("kernel=tall") and f"tile={strip}x" in desc, desc
+    assert err <= O.TOLERANCE[dtype], err

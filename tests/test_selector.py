@@ -4,7 +4,7 @@ import pytest
 from cmp_ext_amd import cabi
 
 K_TILE256, K_TILE224, K_TILE128, K_SKINNY, K_F32_128, K_F32_64, K_GENERIC, K_SKINNY_WIDE, K_F32_96, K_TILE64, \
-    K_SKINNY_NK, K_F32_64K4, K_F32_16K4, K_STREAM, K_STREAM128 = range(15)
+    K_SKINNY_NK, K_F32_64K4, K_F32_16K4, K_STREAM, K_STREAM128, K_TALL = range(16)
 
 
 @pytest.mark.parametrize("dtype,M,N,K,expect", [
@@ -219,6 +219,26 @@ def test_zero_sizes_are_valid():
         assert kid >= 0
 
 
+@pytest.mark.parametrize("layout,M,N,K,batch,expect,strip", [
+    (cabi.B_KN, 2048, 64, 2048, 8, K_TALL, 64),       # attention's P V: 128 tiles of 128 rows, 256 strips of 64
+    (cabi.B_NK, 2048, 64, 2048, 1, K_TALL, 32),       # 16 tiles: 64 strips of 32 rows
+    (cabi.B_NK, 16384, 16, 4096, 1, K_TALL, 64),      # a LoRA down-projection / router, K = 4096
+    (cabi.B_KN, 16384, 64, 1024, 1, K_TALL, 32),      # K < 2048: 32-row strips, two per CU
+    (cabi.B_KN, 4096, 64, 4096, 1, K_TILE128, 0),     # K = 4096 below 8192 rows: the split tile
+    (cabi.B_NK, 16384, 64, 8192, 1, K_TILE128, 0),    # K = 8192: the split tile
+    (cabi.B_KN, 32768, 64, 1024, 1, K_TILE128, 0),    # 256 tiles already fill the GPU
+    (cabi.B_KN, 1024, 64, 1024, 32, K_TILE128, 0),    # ... over a batch
+    (cabi.B_KN, 2048, 128, 2048, 8, K_TILE128, 0),    # 128 columns: measured slower
+    (cabi.B_KN, 2048, 60, 2048, 1, K_GENERIC, 0),     # [K, N] rows not in 16-byte chunks (no workspace)
+    (cabi.B_NK, 2048, 60, 2048, 1, K_TALL, 32),       # ... which B as [N, K] does not need
+])
+def test_tall_kernel_for_narrow_b(layout, M, N, K, batch, expect, strip):
+    kid, desc = cabi.plan(cabi.F16, layout, M, N, K, batch=batch, workspace_bytes=0 if expect == K_GENERIC else 1 << 40)
+    assert kid == expect, desc
+    if expect == K_TALL:
+        assert f"tile={strip}x64 " in desc and "mb=4" in desc and f"grid={-(-M // strip)}x1x{batch}" in desc, desc
+
+
 def test_gemm_config_override(monkeypatch):
     """CMPEXT3_GEMM_CONFIG forces a kernel (and a K split) where that kernel's requirements
     hold for the call, and is ignored otherwise."""
@@ -243,6 +263,16 @@ def test_gemm_config_override(monkeypatch):
     assert not cabi.plan(cabi.F16, cabi.B_KN, 200, 1000, 96, has_bias=True)[1].startswith("kernel=stream")
     assert cabi.plan(cabi.F16, cabi.B_NK, 200, 1000, 96)[1].startswith("kernel=stream128x128")
     assert not cabi.plan(cabi.F16, cabi.B_KN, 200, 1000, 264)[1].startswith("kernel=stream")
+    # the tall kernel (N <= 128; 16-row blocks of B's columns: 4 up to 64, else 8), with the
+    # strip height asked for; not for wider B or [K, N] rows not in 16-byte chunks
+    monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=tall,strip=32")
+    desc = cabi.plan(cabi.BF16, cabi.B_KN, 1000, 72, 200, batch=3)[1]
+    assert desc.startswith("kernel=tall") and "tile=32x128 grid=32x1x3" in desc and "mb=8" in desc, desc
+    monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=tall")
+    desc = cabi.plan(cabi.F16, cabi.B_NK, 100, 20, 40)[1]
+    assert desc.startswith("kernel=tall") and "tile=64x64 grid=2x1x1" in desc and "mb=4" in desc, desc
+    assert not cabi.plan(cabi.F16, cabi.B_KN, 1000, 136, 200)[1].startswith("kernel=tall")
+    assert not cabi.plan(cabi.F16, cabi.B_KN, 1000, 60, 200)[1].startswith("kernel=tall")
     # the generic kernel, with no padded copies in its place
     monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=generic64x64")
     desc = cabi.plan(cabi.BF16, cabi.B_KN, 2048, 2048, 2047, workspace_bytes=ws)[1]

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from cmp_ext_amd import cabi
-from sweep_cases import CASES, CODE, DT, check, describe_case, logical, make_buffers, output_mask, reference
+from sweep_cases import CASES, CODE, DT, N_TALL, check, describe_case, logical, make_buffers, output_mask, reference
 
 BASE = 1 << 32  # a 4 KiB-aligned host address standing in for each buffer
 ESZ = {"fp16": 2, "bf16": 2, "fp32": 4}
@@ -37,7 +37,9 @@ def test_every_sweep_case_is_accepted_and_the_families_are_reached():
         assert ws >= 0 and (c["workspace"] or ws == 0), describe_case(c)
         k = cabi.describe(call)[1].split()[0].split("=")[1]
         kernels[k] = kernels.get(k, 0) + 1
-    assert len(kernels) >= 12, kernels
+        if c["idx"] >= len(CASES) - N_TALL:
+            assert k == "tall", describe_case(c)
+    assert len(kernels) >= 13, kernels
 
 
 def _emulated(c, a, b, bias, cbuf):
