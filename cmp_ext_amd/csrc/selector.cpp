@@ -166,6 +166,38 @@ int forced_splits(const Request& r, int s, int64_t* ksplit) {
   return s;
 }
 
+// skinny_nk (M <= 64, B as [N, K]): strips of W rows over all of K, or over K ranges of
+// `splits` (fp32 partials in the workspace, N % 4 == 0; a split that does not fit the
+// workspace is dropped).  16-row strips when 32-row ones would leave CUs idle.  With more
+// than 16 rows of A every workgroup re-reads all of A from L2 (for 64 x 4096: twice W's
+// bytes over 448 strips of a 14336-row W), so 64-row strips there once they still give
+// >= 192 workgroups (MI355X, x[M, 4096] W[14336, 4096]^T: M = 32 27.7 -> 23.9 us, 48 30.2
+// -> 26.8, 64 34.1 -> 29.3; x[64, 8192] W[14336, 8192]^T 56.8 -> 51.6; x[64, 8192]
+// W[28672, 8192]^T 111 either way).
+Plan skinny_nk_plan(const Request& r, int64_t splits, int group_m) {
+  Plan q{};
+  q.kernel = kSkinnyNK;
+  q.group_m = group_m;
+  q.threads = 256;
+  q.splits = 1;
+  q.mb = (int)std::max<int64_t>(1, cdiv(r.M, 16));
+  q.bm = 16 * q.mb;
+  const int64_t chunk = std::min<int64_t>(r.batch, 65535);
+  q.bn = cdiv(r.N, 32) * chunk >= kNumCUs ? 32 : 16;
+  if (q.mb >= 2 && cdiv(r.N, 64) * chunk >= 192) q.bn = 64;
+  if (splits > 1 && r.N % 4 == 0 && r.K > 256) {
+    const int64_t ks = cdiv(cdiv(r.K, splits), 256) * 256;
+    const int64_t s = cdiv(r.K, ks);
+    const int64_t need = s * r.batch * r.M * r.N * 4;
+    if (s > 1 && need <= r.ws_bytes) {
+      q.splits = (int)s;
+      q.ksplit = (int)ks;
+      q.ws_bytes = need;
+    }
+  }
+  return q;
+}
+
 // The tall kernel for N <= 128 (16-row blocks of B's columns: 4 up to 64 columns, else 8)
 // with strips of `strip` rows of A.
 Plan tall_plan(const Request& r, int strip, int group_m) {
@@ -181,9 +213,9 @@ Plan tall_plan(const Request& r, int strip, int group_m) {
 }
 
 // Applies the override to a 16-bit plan: a tiled kernel (optionally split) when `fast`,
-// the streaming kernel when `stream_ok`, the tall kernel when `tall_ok`, the generic
-// kernel always.
-void override16(const Request& r, bool fast, bool stream_ok, bool tall_ok, Plan* p) {
+// the streaming kernel when `stream_ok`, the tall kernel when `tall_ok`, skinny_nk
+// (optionally split) when `skinny_nk_ok`, the generic kernel always.
+void override16(const Request& r, bool fast, bool stream_ok, bool tall_ok, bool skinny_nk_ok, Plan* p) {
   const Override o = read_override();
   if (o.kernel < 0) return;
   Plan q{};
@@ -220,6 +252,10 @@ void override16(const Request& r, bool fast, bool stream_ok, bool tall_ok, Plan*
       q.bm = 64;
       q.bn = 64;
       q.forced = true;  // no padded copies in its place
+      break;
+    case kSkinnyNK:
+      if (!skinny_nk_ok) return;
+      q = skinny_nk_plan(r, o.splits, p->group_m);
       break;
     case kTall:
       if (!tall_ok) return;
@@ -339,18 +375,17 @@ int make_plan_core(const Request& r, Plan* plan) {
                          (r.layout == kNK || r.N % 8 == 0) &&
                          (!batched || (r.stride_a % 8 == 0 && r.stride_b % 8 == 0));
     if (skinny_ok && !skinny_tiles_enough && r.layout == kNK) {
-      // B is [N, K] (a Linear weight): strips of W rows over all of K; 16-row
-      // strips when 32-row ones would leave CUs idle.  With more than 16 rows of A every
-      // workgroup re-reads all of A from L2 (for 64 x 4096: twice W's bytes over 448 strips
-      // of a 14336-row W), so 64-row strips there once they still give >= 192 workgroups
-      // (MI355X, x[M, 4096] W[14336, 4096]^T: M = 32 27.7 -> 23.9 us, 48 30.2 -> 26.8, 64
-      // 34.1 -> 29.3; x[64, 8192] W[14336, 8192]^T 56.8 -> 51.6; x[64, 8192]
-      // W[28672, 8192]^T 111 either way).
-      p.mb = (int)std::max<int64_t>(1, cdiv(r.M, 16));
-      p.bm = 16 * p.mb;
-      p.kernel = kSkinnyNK;
-      p.bn = cdiv(r.N, 32) * std::min<int64_t>(r.batch, 65535) >= kNumCUs ? 32 : 16;
-      if (p.mb >= 2 && cdiv(r.N, 64) * std::min<int64_t>(r.batch, 65535) >= 192) p.bn = 64;
+      // B is [N, K] (a Linear weight): strips of W rows.  With fewer strips than CUs and
+      // >= 600 KB to stream per workgroup (its W rows and A's 16-row blocks over all of K),
+      // K is split so that ~256 workgroups run: a split costs a second launch (~3 us) and
+      // saves streaming time in proportion (MI355X, fp16, unsplit vs split: x[1, 14336]
+      // W[1024, 14336]^T 14.5 vs 10.5 us (4 ways), x[16, 14336] W[512, 14336]^T 18.9 vs
+      // 10.9 (8), x[64, 4096] W[1024, 4096]^T 12.9 vs 11.1 (4), x[64, 14336] W[2048,
+      // 14336]^T 37.9 vs 25.6 (2); at 520 KB or less the split was slower or even).
+      p = skinny_nk_plan(r, 1, p.group_m);
+      const int64_t wgs = cdiv(r.N, p.bn) * std::min<int64_t>(r.batch, 65535);
+      if (wgs < kNumCUs && (int64_t)(p.bn + p.bm) * r.K * 2 >= 600000)
+        p = skinny_nk_plan(r, std::min<int64_t>(8, std::max<int64_t>(2, kNumCUs / wgs)), p.group_m);
     } else if (skinny_ok && !skinny_tiles_enough) {
       p.mb = (int)std::max<int64_t>(1, cdiv(r.M, 16));
       p.bm = 16 * p.mb;
@@ -443,7 +478,7 @@ int make_plan_core(const Request& r, Plan* plan) {
       p.bm = 64;
       p.bn = 64;
     }
-    override16(r, fast, stream_ok, tall_ok, &p);
+    override16(r, fast, stream_ok, tall_ok, skinny_ok && r.layout == kNK, &p);
   }
   if (p.splits == 0) p.splits = 1;
   if (p.kernel == kSkinny || p.kernel == kSkinnyWide || p.kernel == kSkinnyNK || p.kernel == kStream64x128 ||

@@ -252,14 +252,19 @@ __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int strip = strip_order(blockIdx.x, gridDim.x);
   const int n0 = strip * SW;
-  const int K = p.K;
+  // split K (p.splits > 1): grid.z = batch * splits, split ks sums k in [ks*ksplit, +ksplit)
+  // and writes fp32 partials[ks][batch][M][N] (summed, biased and rounded by a second launch)
+  const int splits = p.splits > 1 ? p.splits : 1;
+  const int ks = (int)blockIdx.z % splits;
+  const int64_t bz = (int)blockIdx.z / splits;
+  const int kbeg = ks * p.ksplit;
+  const int K = splits > 1 ? min(p.K - kbeg, p.ksplit) : p.K;
   // W: the streamed operand (B's rows, or A's when SWAP); X: the small one (A, or B)
   const int w_rows = SWAP ? p.M : p.N, x_rows = SWAP ? p.N : p.M;
-  const int64_t bz = blockIdx.z;
   const int64_t ldw = SWAP ? p.lda : p.ldb, ldx = SWAP ? p.ldb : p.lda;
-  const T* Wb = SWAP ? (const T*)p.A + bz * p.stride_a + (int64_t)n0 * ldw
-                     : (const T*)p.B + bz * p.stride_b + (int64_t)n0 * ldw;
-  const T* Xb = SWAP ? (const T*)p.B + bz * p.stride_b : (const T*)p.A + bz * p.stride_a;
+  const T* Wb = (SWAP ? (const T*)p.A + bz * p.stride_a : (const T*)p.B + bz * p.stride_b) + (int64_t)n0 * ldw + kbeg;
+  const T* Xb = (SWAP ? (const T*)p.B + bz * p.stride_b : (const T*)p.A + bz * p.stride_a) +
+                (XKN ? (int64_t)kbeg * ldx : (int64_t)kbeg);
 
   // ---- DMA sources: rows of PITCH bytes, chunk c of row r stored at chunk c ^ (r % 16) ----
   auto geom = [&](int piece, int& row, int& chunk) {
@@ -371,6 +376,7 @@ __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p)
   // acc[h][mb][r] = (X row 16*mb + c) . (W row n0 + 16*h + 4*g + r)
   float* red = (float*)smem;
   T* Cb = (T*)p.C + bz * p.stride_c;
+  float* part = splits > 1 ? p.partials + ((int64_t)ks * (gridDim.z / splits) + bz) * p.M * p.N : nullptr;
   const uint16_t* bias = (const uint16_t*)p.bias;
   if constexpr (SWAP) {
     // red[wave][W row][X row], rows of RP floats; C[n0 + W row][X row]
@@ -389,6 +395,10 @@ __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p)
       float s = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) s += red[(w * SW + wr) * RP + xr];
+      if (part) {
+        part[(int64_t)m * p.N + xr] = s;
+        continue;
+      }
       if (bias) s += from_bits<T>(bias[p.bias_row ? m : xr]);
       ((uint16_t*)(Cb + (int64_t)m * p.ldc))[xr] = to_bits<T>(s);
     }
@@ -408,6 +418,10 @@ __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p)
       float s = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) s += red[(w * MB * 16 + row) * SW + col];
+      if (part) {
+        part[(int64_t)row * p.N + n] = s;
+        continue;
+      }
       if (bias) s += from_bits<T>(bias[p.bias_row ? row : n]);
       ((uint16_t*)(Cb + (int64_t)row * p.ldc))[n] = to_bits<T>(s);
     }

@@ -340,6 +340,50 @@ def test_skinny_nk_wide_strips(dtype, M, N, K, bias):
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("M,N,K,splits", [(1, 1024, 14336, 4), (24, 512, 14336, 8), (64, 1000, 4104, 4),
+                                          (64, 2048, 14336, 2)])
+def test_skinny_nk_split_k(dtype, M, N, K, splits):
+    """Decode-shaped Linear with few strips of W and long rows: K split over workgroups
+    (fp32 partials, then the reduction adds the column bias and rounds), against the
+    oracle; repeated calls bit-identical."""
+    g = torch.Generator().manual_seed(M + N + K)
+    x = (torch.randn(M, K, generator=g) / np.sqrt(K)).to(DT[dtype]).cuda()
+    w = torch.randn(N, K, generator=g).to(DT[dtype]).cuda()
+    b = torch.randn(N, generator=g).to(DT[dtype]).cuda()
+    print(f"skinny_nk split {dtype} M={M} N={N} K={K}", flush=True)
+    out = cmpext3.linear(x, w, b)
+    name, desc = launched()
+    assert name == "skinny_nk" and f"splits={splits} " in desc, desc
+    torch.cuda.synchronize()
+    ref = O.linear_f64(O.to_f64(x.cpu()), O.to_f64(w.cpu()), O.to_f64(b.cpu()))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    for _ in range(3):
+        assert torch.equal(out, cmpext3.linear(x, w, b))
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_skinny_nk_split_k_batched_c_abi(dtype):
+    """The split over a batch through the C ABI (grid.z = batch x splits, partials per
+    split and entry), C rows 8 apart wider than N, each entry against the oracle."""
+    g = torch.Generator().manual_seed(5)
+    Bn, M, N, K = 3, 16, 256, 14336
+    a = (torch.randn(Bn, M, K, generator=g) / np.sqrt(K)).to(DT[dtype]).cuda()
+    w = torch.randn(Bn, N, K, generator=g).to(DT[dtype]).cuda()
+    c = torch.full((Bn, M, N + 8), float("nan"), dtype=DT[dtype], device="cuda")
+    ws = torch.empty(1 << 24, dtype=torch.uint8, device="cuda")
+    print(f"skinny_nk split C ABI {dtype} {Bn}x{M}x{N}x{K}", flush=True)
+    st, name, desc = cabi_call(CODE[dtype], cabi.B_NK, a, K, M * K, w, K, N * K, c, N + 8, M * (N + 8), None,
+                               M, N, K, Bn, workspace=ws)
+    assert st == cabi.OK and name == "skinny_nk" and "splits=" in desc, desc
+    torch.cuda.synchronize()
+    got = c.cpu()
+    assert torch.isnan(got[:, :, N:].float()).all()
+    for i in range(Bn):
+        ref = O.linear_f64(O.to_f64(a[i].cpu()), O.to_f64(w[i].cpu()))
+        assert O.rel_frobenius(O.to_f64(got[i, :, :N]), ref) <= O.TOLERANCE[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_tall_narrow_b_through_the_operators(dtype):
     """A narrow B under few 128-row tiles runs on strips of A's rows (the tall kernel):
     attention's P V through bmm (B as [K, N], 64-row strips over a batch), a router-shaped

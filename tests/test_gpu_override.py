@@ -40,9 +40,10 @@ def _run(dtype, M, N, K, batch, shared_a, bias, workspace, seed, nk=False, ldc=N
     c = cfull[:, :, :N]
     ag = a.cuda()
     bg = b.transpose(1, 2).contiguous().cuda() if nk else b.cuda()
+    bvg = None if bv is None else bv.cuda()  # held until the call has run (prepare keeps the pointer)
     st, call = cabi.prepare(CODE[dtype], cabi.B_NK if nk else cabi.B_KN, ag, K, 0 if shared_a else M * K,
                             bg, K if nk else N, K * N, c, ldc, M * ldc,
-                            None if bv is None else bv.cuda(), M, N, K, batch,
+                            bvg, M, N, K, batch,
                             cabi.BIAS_PER_ROW if bias == "row" else 0, (1 << 40) if workspace else 0)
     assert st == cabi.OK
     _, desc = cabi.describe(call)
@@ -118,3 +119,12 @@ def test_forced_tall(monkeypatch, dtype, M, N, K, batch, bias, nk, strip, ldc):
     desc, err = _run(dtype, M, N, K, batch, False, bias, False, M + N + K, nk=nk, ldc=ldc)
     assert desc.startswith("kernel=tall") and f"tile={strip}x" in desc, desc
     assert err <= O.TOLERANCE[dtype], err
+
+
+def test_forced_skinny_nk_split(monkeypatch):
+    """skinny_nk with a forced 3-way split of a ragged K (ranges of 1536, 1536, 1032) and a
+    bias per row (added by the reduction), over a batch."""
+    monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=skinny_nk,splits=3")
+    desc, err = _run("bf16", 40, 296, 4104, 2, False, "row", True, 12, nk=True)
+    assert desc.startswith("kernel=skinny_nk") and "splits=3 ksplit=1536" in desc, desc
+    assert err <= O.TOLERANCE["bf16"], err
