@@ -594,7 +594,14 @@ def main() -> int:
     ap.add_argument("--conv-shape", default=None, metavar="B,CIN,H,W,COUT",
                     help="time cmpext3.conv2d 1x1 (with bias) on this shape instead and print its JSON "
                          "object, as --caller does (for profiling the streaming kernel on other shapes)")
-    ap.add_argument("--conv-dtype", default="fp16", choices=["fp16", "bf16", "fp32"])
+    ap.add_argument("--bmm-shape", default=None, metavar="B,M,N,K",
+                    help="time cmpext3.bmm on [B,M,K] @ [B,K,N] instead and print its JSON object, as --caller "
+                         "does (for profiling the kernel chosen for other shapes)")
+    ap.add_argument("--linear-shape", default=None, metavar="M,N,K",
+                    help="time cmpext3.linear (with bias) on x[M,K] @ W[N,K]^T instead, as --bmm-shape does")
+    ap.add_argument("--conv-dtype", "--shape-dtype", dest="conv_dtype", default="fp16",
+                    choices=["fp16", "bf16", "fp32"],
+                    help="dtype of --conv-shape, --bmm-shape and --linear-shape")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of GEMMs, run a plain device copy of MIB MiB per step (reference "
                          "point for rocprofv3 FETCH_SIZE/WRITE_SIZE scaling)")
@@ -627,6 +634,22 @@ def main() -> int:
         name = f"conv1x1_{args.conv_dtype}_{Bn}x{cin}x{h}x{w}_to{cout}"
         CALLERS[name] = dict(op="conv", dtype=args.conv_dtype, M=cout, N=h * w, K=cin, batch=Bn, H=h, hbm=True,
                              desc=f"cmpext3.conv2d 1x1 with bias: input [{Bn},{cin},{h},{w}] -> {cout} channels")
+        args.caller = name
+    for opt, op in ((args.bmm_shape, "bmm"), (args.linear_shape, "linear")):
+        if not opt:
+            continue
+        try:
+            dims = [int(x) for x in opt.split(",")]
+            Bn, M, N, K = dims if op == "bmm" else [1] + dims
+        except ValueError:
+            raise SystemExit(f"bench.py: --{op}-shape takes {'B,M,N,K' if op == 'bmm' else 'M,N,K'} (integers)")
+        name = f"{op}_{args.conv_dtype}_" + "x".join(str(d) for d in dims)
+        c = dict(op=op, dtype=args.conv_dtype, M=M, N=N, K=K, batch=Bn,
+                 desc=f"cmpext3.{op} " + (f"[{Bn},{M},{K}] @ [{Bn},{K},{N}]" if op == "bmm" else
+                                          f"x[{M},{K}] @ W[{N},{K}]^T + b"))
+        flops, nbytes = caller_algorithmic(c)
+        c["hbm"] = flops / nbytes < PEAK[args.conv_dtype] * 1e12 / (HBM_PEAK_GBS * 1e9)  # below the ridge
+        CALLERS[name] = c
         args.caller = name
     if args.caller:
         log(f"timing {args.caller} ({args.warmup} warm-up + {args.steps} steps)")

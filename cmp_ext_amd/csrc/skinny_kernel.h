@@ -250,13 +250,20 @@ __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int strip = strip_order(blockIdx.x, gridDim.x);
+  // Workgroup w (x fastest, then z) runs on XCD w % 8: each XCD takes a contiguous range of
+  // (z, strip) in z-major order, so its L2 holds the small operand of one or two batch
+  // entries (or K ranges) rather than of all of them.
+  const int64_t wg = blockIdx.x + (int64_t)gridDim.x * blockIdx.z, total = (int64_t)gridDim.x * gridDim.z;
+  const int64_t xcd = wg & 7, base = total >> 3, rem = total & 7;
+  const int64_t order = xcd * base + (xcd < rem ? xcd : rem) + (wg >> 3);
+  const int zz = (int)(order / gridDim.x);
+  const int strip = (int)(order - (int64_t)zz * gridDim.x);
   const int n0 = strip * SW;
   // split K (p.splits > 1): grid.z = batch * splits, split ks sums k in [ks*ksplit, +ksplit)
   // and writes fp32 partials[ks][batch][M][N] (summed, biased and rounded by a second launch)
   const int splits = p.splits > 1 ? p.splits : 1;
-  const int ks = (int)blockIdx.z % splits;
-  const int64_t bz = (int)blockIdx.z / splits;
+  const int ks = zz % splits;
+  const int64_t bz = zz / splits;
   const int kbeg = ks * p.ksplit;
   const int K = splits > 1 ? min(p.K - kbeg, p.ksplit) : p.K;
   // W: the streamed operand (B's rows, or A's when SWAP); X: the small one (A, or B)
