@@ -33,7 +33,8 @@
 //     the buffer descriptor's range: the hardware writes zeros into LDS.
 //   * The reads of the next sub-step's fragments and the DMA pieces are spread
 //     one per MFMA slot, with a scheduling barrier after every slot.
-//   * Epilogue: fp32 -> T, bias added in fp32 first (per column, or per row);
+//   * Epilogue: fp32 -> T, bias added in fp32 first (per column, or per row;
+//     staged in LDS);
 //     one v_permlane16_swap per dword pairs accumulator blocks j and j+1 so
 //     that every lane holds 8 consecutive columns, and C is written with
 //     16-byte stores covering 64 contiguous bytes of each of 16 rows.
@@ -308,27 +309,42 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
   const int64_t cpitch = p.ldc | (gridDim.z > 1 ? p.stride_c : 0);
   const bool st16 = (cpitch & 7) == 0, st8 = (cpitch & 3) == 0;
   const int mw = m0 + wm * S::WTM, nw = n0 + wn * S::WTN;
+  // The tile's bias values (BN per column, or BM per row) go to LDS first -- one load per
+  // thread, after every wave's last fragment reads -- so that the epilogue's adds wait on
+  // no global load queued behind its own stores.  Per column: four values per thread, one
+  // 8-byte load when all four exist and the bias is 8-byte aligned, else one 2-byte load
+  // each (a descriptor of 2N bytes returns zeros past N); per row: one value per thread.
+  uint16_t* sbias = (uint16_t*)smem;
+  if constexpr (BIAS != 0) {
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if constexpr (BIAS == 1) {
+      if (tid < BN / 4) {
+        const int n = n0 + 4 * tid;
+        const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(bias), 0, 2 * N, kBufWord3);
+        u32x2 bb;
+        if (n + 4 <= N && p.bias_vec) {
+          bb = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(br, (uint32_t)(2 * n), 0, 0));
+        } else {
+          uint32_t h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = buf_load2(br, (uint32_t)(2 * (n + e)));
+          bb = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        }
+        *(u32x2*)(sbias + 4 * tid) = bb;
+      }
+    } else {
+      if (tid < BM) sbias[tid] = m0 + tid < M ? bias[m0 + tid] : (uint16_t)0;
+    }
+    __syncthreads();
+  }
   auto bias_add = [&](int i, int j, f32x4 v) {
     if constexpr (BIAS == 2) {
-      const int m = mw + 16 * i + r16;
-      const float b = m < M ? from_bits<T>(bias[m]) : 0.f;
+      const float b = from_bits<T>(sbias[wm * S::WTM + 16 * i + r16]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] += b;
     } else if constexpr (BIAS == 1) {
-      // four consecutive bias values: one 8-byte load when all four exist and the bias
-      // is 8-byte aligned, else one 2-byte load each (a descriptor of 2N bytes returns
-      // zeros past N)
-      const int n = nw + 16 * j + 4 * G;
-      const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(bias), 0, 2 * N, kBufWord3);
-      u32x2 bb;
-      if (n + 4 <= N && p.bias_vec) {
-        bb = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(br, (uint32_t)(2 * n), 0, 0));
-      } else {
-        uint32_t h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = buf_load2(br, (uint32_t)(2 * (n + e)));
-        bb = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-      }
+      const u32x2 bb = *(const u32x2*)(sbias + wn * S::WTN + 16 * j + 4 * G);
       v[0] += from_bits<T>((uint16_t)(bb.x & 0xFFFF));
       v[1] += from_bits<T>((uint16_t)(bb.x >> 16));
       v[2] += from_bits<T>((uint16_t)(bb.y & 0xFFFF));
