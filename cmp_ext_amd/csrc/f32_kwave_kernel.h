@@ -214,6 +214,17 @@ __global__ void __launch_bounds__(256, BM == 16 ? 4 : 2) gemm_f32_kwave_kernel(c
   const float* rbias = p.bias_row ? (const float*)p.bias : nullptr;
   const bool vec = ((p.ldc | N) & 3) == 0 && ((uintptr_t)((const float*)p.C + bz * p.stride_c) & 15) == 0;
   const __amdgpu_buffer_rsrc_t crs = make_rsrc((float*)p.C + bz * p.stride_c + (int64_t)m0 * p.ldc + n0);
+  // every block's bias values before any store (a load after a store waits for it)
+  f32x4 bb[FM];
+#pragma unroll
+  for (int t = 0; t < FM; ++t) {
+    const int b = FM * wave + t;
+    const int row = 16 * (b >> 2) + r16, col = 16 * (b & 3) + 4 * g;
+    const float bm = (rbias != nullptr && m0 + row < M) ? rbias[m0 + row] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      bb[t][e] = bm + ((bias != nullptr && n0 + col + e < N) ? bias[n0 + col + e] : 0.f);
+  }
 #pragma unroll
   for (int t = 0; t < FM; ++t) {
     const int b = FM * wave + t;
@@ -226,13 +237,8 @@ __global__ void __launch_bounds__(256, BM == 16 ? 4 : 2) gemm_f32_kwave_kernel(c
       if (row_ok && n0 + col < N) *(f32x4*)(part + (int64_t)(m0 + row) * N + n0 + col) = sum[t];
       continue;
     }
-    const float bm = (rbias != nullptr && row_ok) ? rbias[m0 + row] : 0.f;
     f32x4 v = sum[t];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (bias != nullptr) v[e] += (n0 + col + e < N) ? bias[n0 + col + e] : 0.f;
-      if (rbias != nullptr) v[e] += bm;
-    }
+    if (p.bias != nullptr) v += bb[t];  // a bias per column or per row (one is zero in bb)
     if (vec) {
       buf_store16(crs, row_ok && n0 + col < N ? (uint32_t)(row * p.ldc + col) * 4u : kBufOOB, v);
     } else {
