@@ -376,17 +376,18 @@ int make_plan_core(const Request& r, Plan* plan) {
                          (!batched || (r.stride_a % 8 == 0 && r.stride_b % 8 == 0));
     if (skinny_ok && !skinny_tiles_enough && r.layout == kNK) {
       // B is [N, K] (a Linear weight): strips of W rows.  With at most half as many strips
-      // as CUs and >= 600 KB to stream per workgroup (its W rows and A's 16-row blocks over
+      // as CUs and >= 700 KB to stream per workgroup (its W rows and A's 16-row blocks over
       // all of K), K is split so that ~256 workgroups run: a split costs a second launch
-      // (~3 us) and saves streaming time in proportion (MI355X, fp16, unsplit vs split:
-      // x[1, 14336] W[1024, 14336]^T 14.5 vs 10.5 us (4 ways), x[16, 14336] W[512,
-      // 14336]^T 18.9 vs 10.9 (8), x[64, 4096] W[1024, 4096]^T 12.9 vs 11.1 (4), x[64,
-      // 14336] W[2048, 14336]^T 37.9 vs 25.6 (2); at 520 KB or less the split was slower or
-      // even, and with 224 strips (x[64, 4096] W[14336, 4096]^T) 2 ways took 39.2 us
-      // against 29.3).
+      // (~3 us) and saves streaming time in proportion (MI355X, fp16, W from HBM, unsplit vs
+      // split: x[1, 14336] W[1024, 14336]^T 14.5 vs 10.5 us (4 ways), x[16, 14336] W[512,
+      // 14336]^T 18.9 vs 10.9 (8), x[64, 8192] W[512, 8192]^T 20.6 vs 11.0 (8), x[64, 14336]
+      // W[2048, 14336]^T 37.9 vs 25.6 (2)).  Below that the second launch outweighs what
+      // it saves once W stays in the Infinity Cache between calls (x[64, 4096] W[1024,
+      // 4096]^T, 655 KB: 12.9 vs 11.1 us from HBM but 9.9 vs 12.4 cached), and with 224
+      // strips (x[64, 4096] W[14336, 4096]^T) 2 ways took 39.2 us against 29.3.
       p = skinny_nk_plan(r, 1, p.group_m);
       const int64_t wgs = cdiv(r.N, p.bn) * std::min<int64_t>(r.batch, 65535);
-      if (2 * wgs <= kNumCUs && (int64_t)(p.bn + p.bm) * r.K * 2 >= 600000)
+      if (2 * wgs <= kNumCUs && (int64_t)(p.bn + p.bm) * r.K * 2 >= 700000)
         p = skinny_nk_plan(r, std::min<int64_t>(8, std::max<int64_t>(2, kNumCUs / wgs)), p.group_m);
     } else if (skinny_ok && !skinny_tiles_enough) {
       p.mb = (int)std::max<int64_t>(1, cdiv(r.M, 16));

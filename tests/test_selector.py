@@ -241,10 +241,11 @@ def test_tall_kernel_for_narrow_b(layout, M, N, K, batch, expect, strip):
 
 def test_skinny_nk_split_k_rule():
     """skinny_nk splits K when its strips leave half the CUs or more idle and each
-    workgroup would stream >= 600 KB (W rows + A's 16-row blocks over K), into ~256
+    workgroup would stream >= 700 KB (W rows + A's 16-row blocks over K), into ~256
     workgroups (2..8 ways), and only with the workspace for the partials."""
     ws = 1 << 40
-    for M, N, K, expect in [(1, 1024, 14336, 4), (16, 512, 14336, 8), (64, 1024, 4096, 4), (64, 2048, 14336, 2),
+    for M, N, K, expect in [(1, 1024, 14336, 4), (16, 512, 14336, 8), (64, 1024, 8192, 4), (64, 2048, 14336, 2),
+                            (32, 512, 8192, 8), (64, 1024, 4096, 1),
                             (16, 1024, 8192, 1), (64, 1024, 2048, 1), (1, 4096, 14336, 1), (64, 14336, 4096, 1)]:
         kid, desc = cabi.plan(cabi.F16, cabi.B_NK, M, N, K, workspace_bytes=ws)
         assert kid == K_SKINNY_NK, desc
