@@ -21,8 +21,9 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 struct Candidate {
   KernelId id;
   int bm, bn;
-  int occ;     // workgroups a CU runs at once (1 unless the kernel is built for more)
-  double eff;  // relative per-flop throughput of a CU running occ of these tiles (measured)
+  int occ;      // workgroups a CU runs at once (1 unless the kernel is built for more)
+  double eff;   // relative per-flop throughput of a CU running occ of these tiles (measured)
+  double eff1;  // the same with one workgroup on the CU (latency-bound; = eff when occ == 1)
 };
 
 // Modelled cost of a tiled product, optionally with K split s ways (fp32 partials
@@ -30,26 +31,32 @@ struct Candidate {
 // kNumCUs * occ (workgroups are handed out as slots free, and a CU's matrix cores
 // are shared by whatever it holds); a round is worth occ * bm * bn * (K per split) /
 // eff on the busiest CU (measured on MI355X, this tracks the fp32 and 16-bit tile
-// kernels across 512^3 .. 4096^3 and ragged shapes); a split adds writing and
-// reading the partials at ~5 TB/s and ~6 us for the extra launch.  Units per microsecond on MI355X: one round of 256x256 16-bit tiles at
-// K = 4096 takes ~102 us.
+// kernels across 512^3 .. 4096^3 and ragged shapes), except that a last round leaving
+// every CU a single workgroup is worth bm * bn * (K per split) / eff1; a split adds
+// writing and reading the partials at ~5 TB/s and ~6 us for the extra launch.  Units
+// per microsecond on MI355X: one round of 256x256 16-bit tiles at K = 4096 takes ~102 us.
 constexpr double kUnitsPerUs = 65536.0 * 4096.0 / 102.0;
 double split_cost(const Candidate& c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t s,
                   double units_per_us = kUnitsPerUs) {
   const int64_t tiles = cdiv(M, c.bm) * cdiv(N, c.bn) * batch;
-  const double gemm = (double)cdiv(tiles * s, (int64_t)kNumCUs * c.occ) * c.occ * c.bm * c.bn *
-                      (double)cdiv(K, s) / c.eff;
+  const int64_t slots = (int64_t)kNumCUs * c.occ, wgs = tiles * s;
+  const int64_t full = wgs / slots, rem = wgs - full * slots;
+  const double tile = (double)c.bm * c.bn * (double)cdiv(K, s);
+  double gemm = (double)full * c.occ * tile / c.eff;
+  if (rem > 0) gemm += rem <= kNumCUs ? tile / c.eff1 : c.occ * tile / c.eff;
   const double reduce = s > 1 ? ((double)s * batch * M * N * 8.0 / 5e6 + 6.0) * units_per_us : 0.0;
   return gemm + reduce;
 }
 
 
 // Per-area throughput of a CU running the tile, relative to 256x256 (MI355X, fp16
-// 4096^3: 256x256 102.7 us, 128x128 with two workgroups per CU 126.7 us).
+// 4096^3: 256x256 102.7 us, 128x128 with two workgroups per CU 126.7 us; one 128x128
+// workgroup alone on its CU: 128 x 4096 x 4096 unsplit 41.5 us, 8 x 2048 x 128 x 2048
+// 24.1 us, i.e. 0.61 and 0.53).
 const Candidate kTiles16[] = {
-    {kTile256x256, 256, 256, 1, 1.00},
-    {kTile256x224, 256, 224, 1, 0.98},
-    {kTile128x128, 128, 128, 2, 0.81},
+    {kTile256x256, 256, 256, 1, 1.00, 1.00},
+    {kTile256x224, 256, 224, 1, 0.98, 0.98},
+    {kTile128x128, 128, 128, 2, 0.81, 0.57},
 };
 // fp32 tiles.  A CU holds up to `occ` of their workgroups at once and shares its
 // matrix cores among them; how busy it keeps them grows with the number it holds:

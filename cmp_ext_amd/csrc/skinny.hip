@@ -112,17 +112,18 @@ hipError_t launch_skinny_reduce(DType dt, const GemmParams& p, const float* ws, 
   if (p.N % 4 != 0 || splits < 1) return hipErrorInvalidValue;
   const int64_t rows = (int64_t)batch * p.M;
   if (rows <= 0 || p.N <= 0) return hipSuccess;
-  const int V = p.N % 8 == 0 ? 8 : 4;
+  // 8 columns per thread when that still gives >= 16 waves per CU, else 4 (twice the waves:
+  // the sums are latency-bound when few)
+  const int V = p.N % 8 == 0 && rows * (p.N / 8) >= 256ll * 16 * 64 ? 8 : 4;
   const int64_t esz = dt == kF32 ? 4 : 2;
   // C stores of V elements go out in pieces of at most 16 bytes; they need the
   // piece size as alignment of C, of its row pitch and of its batch stride.
   const int64_t align = std::min<int64_t>(16, V * esz);
   const int vec = (uintptr_t)p.C % align == 0 && (p.ldc * esz) % align == 0 &&
                   (batch == 1 || (p.stride_c * esz) % align == 0);
-  const int64_t ry = std::min<int64_t>(rows, 65535);
-  const int64_t rz = (rows + ry - 1) / ry;
-  if (rz > 65535) return hipErrorInvalidConfiguration;
-  const dim3 grid((unsigned)((p.N / V + 255) / 256), (unsigned)ry, (unsigned)rz);
+  // one V-column chunk per thread; past 65536 workgroups the threads loop (grid stride)
+  const int64_t chunks = rows * (p.N / V);
+  const dim3 grid((unsigned)std::min<int64_t>((chunks + 255) / 256, 65536));
   if (dt == kF16)
     launch_reduce<_Float16>(V, p, ws, splits, batch, vec, grid, s);
   else if (dt == kBF16)

@@ -195,69 +195,71 @@ __global__ void __launch_bounds__(256) gemm_skinny_wide_kernel(const GemmParams 
 }
 
 // C = sum over the S partial blocks in the workspace (+ bias), rounded to T.
-// Workgroup (x, y, z) covers row y + z * gridDim.y of the batch * M rows of C
-// (batch entry and row are split once per workgroup, not per thread) and
-// 256 * V consecutive columns of it.  Each thread sums V columns (N % V == 0):
-// V / 4 16-byte loads per split, the loads of several splits in flight at
-// once, and writes them with V * sizeof(T)-byte stores (16-byte pieces) when
-// `vec` says C's rows and batch entries keep those stores aligned, else
-// element by element.
+// Thread t of the grid-stride loop sums V consecutive columns (N % V == 0) of one row of
+// the batch * M rows: chunk idx = row * (N / V) + column / V, so that a workgroup covers
+// several rows when N is small (one row per workgroup left 240 of 256 threads idle at N =
+// 128).  V / 4 16-byte loads per split, several splits in flight at once; the V results go
+// out as V * sizeof(T)-byte stores (16-byte pieces) when `vec` says C's rows and batch
+// entries keep those stores aligned, else element by element.  The splits are summed in
+// order 0, 1, ..: the result does not depend on the launch geometry.
 template <typename T, int V>
 __global__ void __launch_bounds__(256) skinny_reduce_kernel(const GemmParams p, const float* ws, int splits,
                                                             int batch, int vec) {
   static_assert(V == 4 || V == 8, "4 or 8 columns per thread");
   const int M = p.M, N = p.N;
-  const int64_t row = blockIdx.y + (int64_t)blockIdx.z * gridDim.y;
-  if (row >= (int64_t)batch * M) return;
-  const int n = (blockIdx.x * 256 + threadIdx.x) * V;
-  if (n >= N) return;
-  const int64_t bz = row / M;
-  const int m = (int)(row - bz * M);
+  const int64_t nv = N / V, total = (int64_t)batch * M * nv;
   const int64_t split_stride = (int64_t)batch * M * N;  // floats between one split's block and the next
-  const float* w = ws + row * N + n;
-  f32x4 s[V / 4];
+  for (int64_t idx = blockIdx.x * 256ll + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+    const int64_t row = idx / nv;
+    const int n = (int)(idx - row * nv) * V;
+    const int64_t bz = row / M;
+    const int m = (int)(row - bz * M);
+    const float* w = ws + row * N + n;
+    f32x4 s[V / 4];
 #pragma unroll
-  for (int v = 0; v < V / 4; ++v) s[v] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int v = 0; v < V / 4; ++v) s[v] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
-  for (int sp = 0; sp < splits; ++sp) {
+    for (int sp = 0; sp < splits; ++sp) {
 #pragma unroll
-    for (int v = 0; v < V / 4; ++v) s[v] += *(const f32x4*)(w + sp * split_stride + 4 * v);
-  }
-  float x[V];
-#pragma unroll
-  for (int r = 0; r < V; ++r) x[r] = s[r / 4][r % 4];
-  if constexpr (std::is_same<T, float>::value) {  // fp32 products (split-K fp32 tiles)
-    const float* bias = (const float*)p.bias;
-    if (bias) {
-#pragma unroll
-      for (int r = 0; r < V; ++r) x[r] += bias[p.bias_row ? m : n + r];
+      for (int v = 0; v < V / 4; ++v) s[v] += *(const f32x4*)(w + sp * split_stride + 4 * v);
     }
-    float* crow = (float*)p.C + bz * p.stride_c + (int64_t)m * p.ldc + n;
-    if (vec) {
+    float x[V];
 #pragma unroll
-      for (int v = 0; v < V / 4; ++v) *(f32x4*)(crow + 4 * v) = f32x4{x[4 * v], x[4 * v + 1], x[4 * v + 2], x[4 * v + 3]};
+    for (int r = 0; r < V; ++r) x[r] = s[r / 4][r % 4];
+    if constexpr (std::is_same<T, float>::value) {  // fp32 products (split-K fp32 tiles)
+      const float* bias = (const float*)p.bias;
+      if (bias) {
+#pragma unroll
+        for (int r = 0; r < V; ++r) x[r] += bias[p.bias_row ? m : n + r];
+      }
+      float* crow = (float*)p.C + bz * p.stride_c + (int64_t)m * p.ldc + n;
+      if (vec) {
+#pragma unroll
+        for (int v = 0; v < V / 4; ++v)
+          *(f32x4*)(crow + 4 * v) = f32x4{x[4 * v], x[4 * v + 1], x[4 * v + 2], x[4 * v + 3]};
+      } else {
+#pragma unroll
+        for (int r = 0; r < V; ++r) crow[r] = x[r];
+      }
     } else {
+      const uint16_t* bias = (const uint16_t*)p.bias;
+      if (bias) {
 #pragma unroll
-      for (int r = 0; r < V; ++r) crow[r] = x[r];
-    }
-  } else {
-    const uint16_t* bias = (const uint16_t*)p.bias;
-    if (bias) {
+        for (int r = 0; r < V; ++r) x[r] += from_bits<T>(bias[p.bias_row ? m : n + r]);
+      }
+      uint16_t* crow = (uint16_t*)((T*)p.C + bz * p.stride_c + (int64_t)m * p.ldc + n);
+      if (vec) {
+        uint32_t q[V / 2];
 #pragma unroll
-      for (int r = 0; r < V; ++r) x[r] += from_bits<T>(bias[p.bias_row ? m : n + r]);
-    }
-    uint16_t* crow = (uint16_t*)((T*)p.C + bz * p.stride_c + (int64_t)m * p.ldc + n);
-    if (vec) {
-      uint32_t q[V / 2];
+        for (int v = 0; v < V / 2; ++v) q[v] = (uint32_t)to_bits<T>(x[2 * v]) | ((uint32_t)to_bits<T>(x[2 * v + 1]) << 16);
+        if constexpr (V == 8)
+          *(u32x4*)crow = u32x4{q[0], q[1], q[2], q[3]};
+        else
+          *(u32x2*)crow = u32x2{q[0], q[1]};
+      } else {
 #pragma unroll
-      for (int v = 0; v < V / 2; ++v) q[v] = (uint32_t)to_bits<T>(x[2 * v]) | ((uint32_t)to_bits<T>(x[2 * v + 1]) << 16);
-      if constexpr (V == 8)
-        *(u32x4*)crow = u32x4{q[0], q[1], q[2], q[3]};
-      else
-        *(u32x2*)crow = u32x2{q[0], q[1]};
-    } else {
-#pragma unroll
-      for (int r = 0; r < V; ++r) crow[r] = to_bits<T>(x[r]);
+        for (int r = 0; r < V; ++r) crow[r] = to_bits<T>(x[r]);
+      }
     }
   }
 }
