@@ -443,7 +443,7 @@ int make_plan_core(const Request& r, Plan* plan) {
       // 16.6 vs 25.0, 16384 x 16 x 4096 27.7 vs 30.7, attention's P V over 8 x 2048 x 2048
       // with 64 columns 18.8 vs 25.7; measured slower from K = 8192, with 64 < N <= 128, or
       // at K = 4096 below 8192 rows).  64-row strips once they give every CU one and K >=
-      // 2048, else 32-row strips two workgroups per CU.
+      // 2048, else 32-row strips.
       p = tall_plan(r, cdiv(r.M, 64) * r.batch >= kNumCUs && r.K >= 2048 ? 64 : 32, p.group_m);
     } else if (fast && r.M <= 64 && r.K <= 1024 && cdiv(r.N, 256) * r.batch >= kNumCUs) {
       // Short-K products with few rows and many columns are HBM-bound; 64-row tiles

@@ -8,13 +8,15 @@
 
 namespace cmpext3 {
 namespace {
-// KS = 128 k per stage: strip rows of 256 bytes, B k-rows of 64 or 128 columns.  32-row
-// strips with B of 64 columns run in a ring of three 24 KiB stages, two workgroups per CU.
+// KS = 128 k per stage: strip rows of 256 bytes, B k-rows of 64 or 128 columns; 32-row
+// strips with B of 64 columns (chosen when there are few strips) take 256 k per stage in a
+// ring of three 48 KiB stages (MI355X, B as [K, N]: 2048 x 64 x 2048 10.0 -> 8.8 us, 8192
+// x 64 x 2048 10.5 -> 9.8 against 128 k in three 24 KiB stages, two workgroups per CU).
 template <typename T, bool XKN, bool NT>
 hipError_t launch_tall_t(int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {
   const dim3 block(256);
   if (mb == 4 && strip == 32)
-    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, 32, 128, NT, 3, true, XKN>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, 32, 256, NT, 3, true, XKN>), grid, block, 0, s, p);
   else if (mb == 4 && strip == 64)
     hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, 64, 128, NT, 8, true, XKN>), grid, block, 0, s, p);
   else if (mb == 8 && strip == 32)
