@@ -214,6 +214,7 @@ Plan tall_plan(const Request& r, int strip, int group_m) {
   q.threads = 256;
   q.splits = 1;
   q.mb = r.N <= 64 ? 4 : 8;
+  if (r.layout == kNK && r.N <= 32) q.mb = r.N <= 16 ? 1 : 2;  // B as [N, K]: 16-row blocks as needed
   q.bm = strip;
   q.bn = 16 * q.mb;
   return q;

@@ -112,6 +112,8 @@ def test_forced_fp32_tile_split(monkeypatch):
     ("bf16", 513, 128, 1032, 1, "row", False, 32, 136),    # 128 columns, 32-row strips
     ("fp16", 2048, 64, 2048, 2, "col", True, 64, None),    # B as [N, K] (a router's weight)
     ("bf16", 1000, 40, 72, 2, None, True, 32, None),       # [N, K], 40 rows, short K
+    ("fp16", 700, 8, 520, 2, "col", True, 64, None),       # [N, K], 8 rows: one 16-row block
+    ("bf16", 1500, 24, 1032, 1, "row", True, 32, 40),      # [N, K], 24 rows: two 16-row blocks
     ("fp16", 129, 128, 520, 3, "row", True, 64, 130),      # [N, K], 128 rows, odd C pitch
 ])
 def test_forced_tall(monkeypatch, dtype, M, N, K, batch, bias, nk, strip, ldc):

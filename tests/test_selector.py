@@ -236,7 +236,10 @@ def test_tall_kernel_for_narrow_b(layout, M, N, K, batch, expect, strip):
     kid, desc = cabi.plan(cabi.F16, layout, M, N, K, batch=batch, workspace_bytes=0 if expect == K_GENERIC else 1 << 40)
     assert kid == expect, desc
     if expect == K_TALL:
-        assert f"tile={strip}x64 " in desc and "mb=4" in desc and f"grid={-(-M // strip)}x1x{batch}" in desc, desc
+        # 16-row blocks of B's columns: 4 for [K, N] (64-column LDS rows); as needed for [N, K]
+        mb = 4 if layout == cabi.B_KN or N > 32 else (1 if N <= 16 else 2)
+        assert f"tile={strip}x{16 * mb} " in desc and f"mb={mb}" in desc, desc
+        assert f"grid={-(-M // strip)}x1x{batch}" in desc, desc
 
 
 def test_skinny_nk_split_k_rule():
@@ -278,13 +281,16 @@ def test_gemm_config_override(monkeypatch):
     assert not cabi.plan(cabi.F16, cabi.B_KN, 200, 1000, 96, has_bias=True)[1].startswith("kernel=stream")
     assert cabi.plan(cabi.F16, cabi.B_NK, 200, 1000, 96)[1].startswith("kernel=stream128x128")
     assert not cabi.plan(cabi.F16, cabi.B_KN, 200, 1000, 264)[1].startswith("kernel=stream")
-    # the tall kernel (N <= 128; 16-row blocks of B's columns: 4 up to 64, else 8), with the
+    # the tall kernel (N <= 128; 16-row blocks of B's columns: 4 up to 64, else 8; for B as
+    # [N, K] 1 up to 16 columns, 2 up to 32), with the
     # strip height asked for; not for wider B or [K, N] rows not in 16-byte chunks
     monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=tall,strip=32")
     desc = cabi.plan(cabi.BF16, cabi.B_KN, 1000, 72, 200, batch=3)[1]
     assert desc.startswith("kernel=tall") and "tile=32x128 grid=32x1x3" in desc and "mb=8" in desc, desc
     monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=tall")
     desc = cabi.plan(cabi.F16, cabi.B_NK, 100, 20, 40)[1]
+    assert desc.startswith("kernel=tall") and "tile=64x32 grid=2x1x1" in desc and "mb=2" in desc, desc
+    desc = cabi.plan(cabi.F16, cabi.B_KN, 100, 16, 40)[1]
     assert desc.startswith("kernel=tall") and "tile=64x64 grid=2x1x1" in desc and "mb=4" in desc, desc
     assert not cabi.plan(cabi.F16, cabi.B_KN, 1000, 136, 200)[1].startswith("kernel=tall")
     assert not cabi.plan(cabi.F16, cabi.B_KN, 1000, 60, 200)[1].startswith("kernel=tall")
