@@ -436,14 +436,16 @@ int make_plan_core(const Request& r, Plan* plan) {
       p.bn = 128;
       p.threads = r.M <= 64 ? 256 : 512;
     } else if (tall_ok && r.N <= 64 && r.M >= 1024 && r.K >= 1024 && cdiv(r.M, 128) * r.batch < kNumCUs &&
-               (r.K <= 2048 || (r.K <= 4096 && r.M * r.batch >= 8192))) {
+               (r.K <= 2048 ||
+                (r.K <= 4096 && (r.M * r.batch >= 8192 || (r.layout == kNK && r.N <= 32))))) {
       // A narrow B (<= 64 columns) under fewer 128-row tiles than CUs: the tile kernels would
       // split K (or leave CUs idle) to fill the GPU; strips of A's rows over all of K stream
       // A once instead (MI355X, fp16, best strip vs the selector's tile128x128 (+ split):
       // 2048 x 64 x 2048 8.5 vs 10.8 us, 8192 x 64 x 2048 10.4 vs 16.1, 16384 x 64 x 2048
       // 16.6 vs 25.0, 16384 x 16 x 4096 27.7 vs 30.7, attention's P V over 8 x 2048 x 2048
       // with 64 columns 18.8 vs 25.7; measured slower from K = 8192, with 64 < N <= 128, or
-      // at K = 4096 below 8192 rows).  64-row strips once they give every CU one and K >=
+      // at K = 4096 below 8192 rows -- except B as [N, K] with <= 32 rows, on one or two
+      // 16-row blocks: 4096 x 16 x 4096 7.9 vs 10.8 us, 1024 x 32 x 4096 8.7 vs 9.4).  64-row strips once they give every CU one and K >=
       // 2048, else 32-row strips.
       p = tall_plan(r, cdiv(r.M, 64) * r.batch >= kNumCUs && r.K >= 2048 ? 64 : 32, p.group_m);
     } else if (fast && r.M <= 64 && r.K <= 1024 && cdiv(r.N, 256) * r.batch >= kNumCUs) {

@@ -225,6 +225,8 @@ def test_zero_sizes_are_valid():
     (cabi.B_NK, 16384, 16, 4096, 1, K_TALL, 64),      # a LoRA down-projection / router, K = 4096
     (cabi.B_KN, 16384, 64, 1024, 1, K_TALL, 32),      # K < 2048: 32-row strips, two per CU
     (cabi.B_KN, 4096, 64, 4096, 1, K_TILE128, 0),     # K = 4096 below 8192 rows: the split tile
+    (cabi.B_NK, 4096, 16, 4096, 1, K_TALL, 32),       # ... unless B is [N, K] with <= 32 rows
+    (cabi.B_NK, 4096, 48, 4096, 1, K_TILE128, 0),
     (cabi.B_NK, 16384, 64, 8192, 1, K_TILE128, 0),    # K = 8192: the split tile
     (cabi.B_KN, 32768, 64, 1024, 1, K_TILE128, 0),    # 256 tiles already fill the GPU
     (cabi.B_KN, 1024, 64, 1024, 32, K_TILE128, 0),    # ... over a batch
