@@ -70,18 +70,20 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
     case kSkinny:
       return launch_skinny((DType)dtype, plan.mb, p, grid, s);
     case kSkinnyNK:
+    case kTall:
       if (plan.splits > 1) {  // split K: fp32 partials, then the reduction adds the bias and rounds
         GemmParams q = p;
         q.splits = plan.splits;
         q.ksplit = plan.ksplit;
         q.partials = (float*)ws;
-        hipError_t e = launch_skinny_nk((DType)dtype, plan.mb, plan.bn, q, dim3(grid.x, grid.y, grid.z * plan.splits), s);
+        const dim3 g(grid.x, grid.y, grid.z * plan.splits);
+        hipError_t e = plan.kernel == kTall ? launch_tall((DType)dtype, lay, plan.mb, plan.bm, q, g, s)
+                                            : launch_skinny_nk((DType)dtype, plan.mb, plan.bn, q, g, s);
         if (e == hipSuccess) e = launch_skinny_reduce((DType)dtype, p, (const float*)ws, plan.splits, (int)grid.z, s);
         return e;
       }
-      return launch_skinny_nk((DType)dtype, plan.mb, plan.bn, p, grid, s);
-    case kTall:
-      return launch_tall((DType)dtype, lay, plan.mb, plan.bm, p, grid, s);
+      return plan.kernel == kTall ? launch_tall((DType)dtype, lay, plan.mb, plan.bm, p, grid, s)
+                                  : launch_skinny_nk((DType)dtype, plan.mb, plan.bn, p, grid, s);
     case kF32Tile128:
     case kF32Tile64:
     case kF32Tile96x64:
@@ -231,7 +233,8 @@ int run(const Prepared& pc, void* workspace, int64_t workspace_bytes, hipStream_
   // kernels whose K split multiplies grid.z (the skinny_wide split goes along grid.x)
   const bool split_z = plan.kernel == kTile256x256 || plan.kernel == kTile256x224 || plan.kernel == kTile128x128 ||
                      plan.kernel == kF32Tile128 || plan.kernel == kF32Tile96x64 || plan.kernel == kF32Tile64 ||
-                     plan.kernel == kF32Tile64K4 || plan.kernel == kF32Tile16K4 || plan.kernel == kSkinnyNK;
+                     plan.kernel == kF32Tile64K4 || plan.kernel == kF32Tile16K4 || plan.kernel == kSkinnyNK ||
+                     plan.kernel == kTall;
   const int64_t zmax = kMaxGridZ / std::max(1, split_z ? plan.splits : 1);
   for (int64_t b0 = 0; b0 < batch; b0 += zmax) {
     const int64_t nb = std::min<int64_t>(zmax, batch - b0);

@@ -207,7 +207,7 @@ Plan skinny_nk_plan(const Request& r, int64_t splits, int group_m) {
 
 // The tall kernel for N <= 128 (16-row blocks of B's columns: 4 up to 64 columns, else 8)
 // with strips of `strip` rows of A.
-Plan tall_plan(const Request& r, int strip, int group_m) {
+Plan tall_plan(const Request& r, int strip, int group_m, int64_t splits = 1) {
   Plan q{};
   q.kernel = kTall;
   q.group_m = group_m;
@@ -217,6 +217,16 @@ Plan tall_plan(const Request& r, int strip, int group_m) {
   if (r.layout == kNK && r.N <= 32) q.mb = r.N <= 16 ? 1 : 2;  // B as [N, K]: 16-row blocks as needed
   q.bm = strip;
   q.bn = 16 * q.mb;
+  if (splits > 1 && r.N % 4 == 0 && r.K > 256) {  // K ranges of whole 256-k stages, fp32 partials
+    const int64_t ks = cdiv(cdiv(r.K, splits), 256) * 256;
+    const int64_t s = cdiv(r.K, ks);
+    const int64_t need = s * r.batch * r.M * r.N * 4;
+    if (s > 1 && need <= r.ws_bytes) {
+      q.splits = (int)s;
+      q.ksplit = (int)ks;
+      q.ws_bytes = need;
+    }
+  }
   return q;
 }
 
@@ -267,7 +277,7 @@ void override16(const Request& r, bool fast, bool stream_ok, bool tall_ok, bool 
       break;
     case kTall:
       if (!tall_ok) return;
-      q = tall_plan(r, o.strip ? o.strip : 64, p->group_m);
+      q = tall_plan(r, o.strip ? o.strip : 64, p->group_m, o.splits);
       break;
     default:
       return;
@@ -448,6 +458,13 @@ int make_plan_core(const Request& r, Plan* plan) {
       // 16-row blocks: 4096 x 16 x 4096 7.9 vs 10.8 us, 1024 x 32 x 4096 8.7 vs 9.4).  64-row strips once they give every CU one and K >=
       // 2048, else 32-row strips.
       p = tall_plan(r, cdiv(r.M, 64) * r.batch >= kNumCUs && r.K >= 2048 ? 64 : 32, p.group_m);
+    } else if (tall_ok && r.N <= 64 && r.M >= 1024 && r.K >= 8192 && cdiv(r.M, 32) * r.batch <= 64 &&
+               r.N % 4 == 0) {
+      // ... and with long K over at most 64 strips of 32 rows, K split so that ~256
+      // workgroups run (fp32 partials, a second launch sums them; MI355X, fp16, vs the
+      // selector's tile128x128 split 16 ways: 1024 x 16 x 14336 9.9 vs 14.3 us, 1024 x 64 x
+      // 14336 13.0 vs 15.5, 2048 x 8 x 14336 13.3 vs 16.4, 1024 x 64 x 8192 10.7 vs 11.6)
+      p = tall_plan(r, 32, p.group_m, std::min<int64_t>(8, kNumCUs / (cdiv(r.M, 32) * r.batch)));
     } else if (fast && r.M <= 64 && r.K <= 1024 && cdiv(r.N, 256) * r.batch >= kNumCUs) {
       // Short-K products with few rows and many columns are HBM-bound; 64-row tiles
       // waste no MFMA rows and keep more loads in flight per CU (MI355X, 64x256 vs

@@ -384,6 +384,37 @@ def test_skinny_nk_split_k_batched_c_abi(dtype):
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_tall_split_k(dtype):
+    """Narrow B with long K over few strips: the tall kernel with K split (fp32 partials,
+    the reduction adds the bias and rounds) -- a router-shaped Linear with a column bias
+    (B as [N, K], 8 ways) and a batched bmm with B as [K, N] (4 ways) -- against the
+    oracle; repeated calls bit-identical."""
+    g = torch.Generator().manual_seed(31)
+    dt = DT[dtype]
+    x = (torch.randn(1024, 14336, generator=g) / np.sqrt(14336)).to(dt).cuda()
+    w = torch.randn(16, 14336, generator=g).to(dt).cuda()
+    b = torch.randn(16, generator=g).to(dt).cuda()
+    print(f"tall split linear {dtype} 1024x16x14336", flush=True)
+    out = cmpext3.linear(x, w, b)
+    name, desc = launched()
+    assert name == "tall" and "splits=8 " in desc, desc
+    torch.cuda.synchronize()
+    ref = O.linear_f64(O.to_f64(x.cpu()), O.to_f64(w.cpu()), O.to_f64(b.cpu()))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    assert torch.equal(out, cmpext3.linear(x, w, b))
+    p = (torch.randn(2, 1024, 8200, generator=g) / np.sqrt(8200)).to(dt).cuda()
+    v = torch.randn(2, 8200, 64, generator=g).to(dt).cuda()
+    print(f"tall split bmm {dtype} 2x1024x64x8200", flush=True)
+    out = cmpext3.bmm(p, v)
+    name, desc = launched()
+    assert name == "tall" and "splits=4 " in desc, desc
+    torch.cuda.synchronize()
+    ref = O.bmm_f64(O.to_f64(p.cpu()), O.to_f64(v.cpu()))
+    assert O.rel_frobenius(O.to_f64(out.cpu()), ref) <= O.TOLERANCE[dtype]
+    assert torch.equal(out, cmpext3.bmm(p, v))
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_tall_narrow_b_through_the_operators(dtype):
     """A narrow B under few 128-row tiles runs on strips of A's rows (the tall kernel):
     attention's P V through bmm (B as [K, N], 64-row strips over a batch), a router-shaped

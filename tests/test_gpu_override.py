@@ -130,3 +130,12 @@ def test_forced_skinny_nk_split(monkeypatch):
     desc, err = _run("bf16", 40, 296, 4104, 2, False, "row", True, 12, nk=True)
     assert desc.startswith("kernel=skinny_nk") and "splits=3 ksplit=1536" in desc, desc
     assert err <= O.TOLERANCE["bf16"], err
+
+
+def test_forced_tall_split(monkeypatch):
+    """The tall kernel with a forced 3-way split of a ragged K (B as [K, N], 64-row strips,
+    a bias per row added by the reduction) over a batch."""
+    monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=tall,strip=64,splits=3")
+    desc, err = _run("fp16", 700, 40, 2056, 2, False, "row", True, 13)
+    assert desc.startswith("kernel=tall") and "splits=3 ksplit=768" in desc, desc
+    assert err <= O.TOLERANCE["fp16"], err

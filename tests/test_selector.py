@@ -244,6 +244,20 @@ def test_tall_kernel_for_narrow_b(layout, M, N, K, batch, expect, strip):
         assert f"grid={-(-M // strip)}x1x{batch}" in desc, desc
 
 
+def test_tall_split_k_rule():
+    """Narrow B, few 32-row strips of A and K >= 8192: the tall kernel with K split so that
+    ~256 workgroups run (8 ways over 32 strips, 4 over 64), with the workspace only."""
+    ws = 1 << 40
+    for lay, M, N, K, B, expect in [(cabi.B_NK, 1024, 16, 14336, 1, 8), (cabi.B_KN, 2048, 64, 8192, 1, 4),
+                                    (cabi.B_KN, 1024, 64, 8192, 2, 4), (cabi.B_NK, 1024, 8, 8192, 1, 8)]:
+        kid, desc = cabi.plan(cabi.F16, lay, M, N, K, batch=B, workspace_bytes=ws)
+        assert kid == K_TALL and "tile=32x" in desc and f"splits={expect} " in desc, desc
+    kid, desc = cabi.plan(cabi.F16, cabi.B_NK, 4096, 16, 14336, workspace_bytes=ws)
+    assert kid == K_TILE128, desc                       # 128 strips: the split tile
+    kid, desc = cabi.plan(cabi.F16, cabi.B_NK, 1024, 16, 14336)
+    assert kid == K_TALL and "splits" not in desc, desc  # no workspace: unsplit strips
+
+
 def test_skinny_nk_split_k_rule():
     """skinny_nk splits K when its strips leave half the CUs or more idle and each
     workgroup would stream >= 700 KB (W rows + A's 16-row blocks over K), into ~256
