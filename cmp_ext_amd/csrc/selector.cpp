@@ -173,6 +173,21 @@ int forced_splits(const Request& r, int s, int64_t* ksplit) {
   return s;
 }
 
+// K split of a strips kernel (skinny_nk, tall): ranges of whole 256-k stages, none empty,
+// fp32 partials [split][batch][M][N] in the workspace (their 16-byte stores need N % 4 ==
+// 0); left unsplit when the workspace is too small.
+void split_strips(const Request& r, int64_t splits, Plan* q) {
+  if (splits <= 1 || r.N % 4 != 0 || r.K <= 256) return;
+  const int64_t ks = cdiv(cdiv(r.K, splits), 256) * 256;
+  const int64_t s = cdiv(r.K, ks);
+  const int64_t need = s * r.batch * r.M * r.N * 4;
+  if (s > 1 && need <= r.ws_bytes) {
+    q->splits = (int)s;
+    q->ksplit = (int)ks;
+    q->ws_bytes = need;
+  }
+}
+
 // skinny_nk (M <= 64, B as [N, K]): strips of W rows over all of K, or over K ranges of
 // `splits` (fp32 partials in the workspace, N % 4 == 0; a split that does not fit the
 // workspace is dropped).  16-row strips when 32-row ones would leave CUs idle.  With more
@@ -192,21 +207,13 @@ Plan skinny_nk_plan(const Request& r, int64_t splits, int group_m) {
   const int64_t chunk = std::min<int64_t>(r.batch, 65535);
   q.bn = cdiv(r.N, 32) * chunk >= kNumCUs ? 32 : 16;
   if (q.mb >= 2 && cdiv(r.N, 64) * chunk >= 192) q.bn = 64;
-  if (splits > 1 && r.N % 4 == 0 && r.K > 256) {
-    const int64_t ks = cdiv(cdiv(r.K, splits), 256) * 256;
-    const int64_t s = cdiv(r.K, ks);
-    const int64_t need = s * r.batch * r.M * r.N * 4;
-    if (s > 1 && need <= r.ws_bytes) {
-      q.splits = (int)s;
-      q.ksplit = (int)ks;
-      q.ws_bytes = need;
-    }
-  }
+  split_strips(r, splits, &q);
   return q;
 }
 
-// The tall kernel for N <= 128 (16-row blocks of B's columns: 4 up to 64 columns, else 8)
-// with strips of `strip` rows of A.
+// The tall kernel for N <= 128 (16-row blocks of B's columns: 4 up to 64 columns, else 8;
+// for B as [N, K] 1 up to 16 and 2 up to 32) with strips of `strip` rows of A, over all of
+// K or over K ranges of `splits`.
 Plan tall_plan(const Request& r, int strip, int group_m, int64_t splits = 1) {
   Plan q{};
   q.kernel = kTall;
@@ -217,16 +224,7 @@ Plan tall_plan(const Request& r, int strip, int group_m, int64_t splits = 1) {
   if (r.layout == kNK && r.N <= 32) q.mb = r.N <= 16 ? 1 : 2;  // B as [N, K]: 16-row blocks as needed
   q.bm = strip;
   q.bn = 16 * q.mb;
-  if (splits > 1 && r.N % 4 == 0 && r.K > 256) {  // K ranges of whole 256-k stages, fp32 partials
-    const int64_t ks = cdiv(cdiv(r.K, splits), 256) * 256;
-    const int64_t s = cdiv(r.K, ks);
-    const int64_t need = s * r.batch * r.M * r.N * 4;
-    if (s > 1 && need <= r.ws_bytes) {
-      q.splits = (int)s;
-      q.ksplit = (int)ks;
-      q.ws_bytes = need;
-    }
-  }
+  split_strips(r, splits, &q);
   return q;
 }
 
