@@ -138,7 +138,7 @@ namespace {
 struct Override {
   int kernel = -1;
   int splits = 1;
-  int strip = 0;  // tall: rows of A per workgroup (32 or 64; 0: the selector's)
+  int strip = 0;  // tall, skinny_nk: rows of A (of W) per workgroup (16, 32 or 64; 0: the selector's)
 };
 
 Override read_override() {
@@ -157,7 +157,7 @@ Override read_override() {
       if (v >= 1 && v <= 16) o.splits = v;
     } else if (strncmp(tok, "strip=", 6) == 0) {
       const int v = atoi(tok + 6);
-      if (v == 32 || v == 64) o.strip = v;
+      if (v == 16 || v == 32 || v == 64) o.strip = v;
     }
   }
   return o;
@@ -272,10 +272,11 @@ void override16(const Request& r, bool fast, bool stream_ok, bool tall_ok, bool 
     case kSkinnyNK:
       if (!skinny_nk_ok) return;
       q = skinny_nk_plan(r, o.splits, p->group_m);
+      if (o.strip) q.bn = o.strip;
       break;
     case kTall:
       if (!tall_ok) return;
-      q = tall_plan(r, o.strip ? o.strip : 64, p->group_m, o.splits);
+      q = tall_plan(r, o.strip == 32 ? 32 : 64, p->group_m, o.splits);
       break;
     default:
       return;
@@ -402,9 +403,22 @@ int make_plan_core(const Request& r, Plan* plan) {
       // 4096]^T, 655 KB: 12.9 vs 11.1 us from HBM but 9.9 vs 12.4 cached), and with 224
       // strips (x[64, 4096] W[14336, 4096]^T) 2 ways took 39.2 us against 29.3.
       p = skinny_nk_plan(r, 1, p.group_m);
-      const int64_t wgs = cdiv(r.N, p.bn) * std::min<int64_t>(r.batch, 65535);
-      if (2 * wgs <= kNumCUs && (int64_t)(p.bn + p.bm) * r.K * 2 >= 700000)
+      const int64_t chunk = std::min<int64_t>(r.batch, 65535);
+      const int64_t wgs = cdiv(r.N, p.bn) * chunk, wgs64 = cdiv(r.N, 64) * chunk;
+      if (2 * wgs <= kNumCUs && (int64_t)(p.bn + p.bm) * r.K * 2 >= 700000) {
         p = skinny_nk_plan(r, std::min<int64_t>(8, std::max<int64_t>(2, kNumCUs / wgs)), p.group_m);
+      } else if (p.mb >= 2 && r.K >= 8192 && 2 * wgs64 <= kNumCUs) {
+        // Long K with more than 16 rows of A over enough narrow strips: each 16-row strip
+        // re-reads all of A from L2 (4x W's bytes at 64 rows), so 64-row strips with K split
+        // to ~256 workgroups instead (MI355X, fp16, W from HBM: x[64, 14336] W[4096,
+        // 14336]^T 40.9 -> 31.3 us, x[32, 14336] W[4096, 14336]^T 29.6 -> 25.7, x[64, 14336]
+        // W[8192, 14336]^T 56.4 -> 50.8; at K = 4096 the unsplit narrow strips stay faster)
+        Plan q = skinny_nk_plan(r, std::max<int64_t>(2, kNumCUs / wgs64), p.group_m);
+        if (q.splits > 1) {
+          q.bn = 64;
+          p = q;
+        }
+      }
     } else if (skinny_ok && !skinny_tiles_enough) {
       p.mb = (int)std::max<int64_t>(1, cdiv(r.M, 16));
       p.bm = 16 * p.mb;

@@ -341,7 +341,7 @@ def test_skinny_nk_wide_strips(dtype, M, N, K, bias):
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("M,N,K,splits", [(1, 1024, 14336, 4), (24, 512, 14336, 8), (64, 1000, 8200, 4),
-                                          (64, 2048, 14336, 2)])
+                                          (64, 2048, 14336, 2), (40, 4096, 10248, 4)])
 def test_skinny_nk_split_k(dtype, M, N, K, splits):
     """Decode-shaped Linear with few strips of W and long rows: K split over workgroups
     (fp32 partials, then the reduction adds the column bias and rounds), against the
