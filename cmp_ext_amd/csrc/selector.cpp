@@ -407,12 +407,13 @@ int make_plan_core(const Request& r, Plan* plan) {
       const int64_t wgs = cdiv(r.N, p.bn) * chunk, wgs64 = cdiv(r.N, 64) * chunk;
       if (2 * wgs <= kNumCUs && (int64_t)(p.bn + p.bm) * r.K * 2 >= 700000) {
         p = skinny_nk_plan(r, std::min<int64_t>(8, std::max<int64_t>(2, kNumCUs / wgs)), p.group_m);
-      } else if (p.mb >= 2 && r.K >= 8192 && 2 * wgs64 <= kNumCUs) {
+      } else if (p.mb >= 2 && r.K >= 10240 && 2 * wgs64 <= kNumCUs) {
         // Long K with more than 16 rows of A over enough narrow strips: each 16-row strip
         // re-reads all of A from L2 (4x W's bytes at 64 rows), so 64-row strips with K split
         // to ~256 workgroups instead (MI355X, fp16, W from HBM: x[64, 14336] W[4096,
         // 14336]^T 40.9 -> 31.3 us, x[32, 14336] W[4096, 14336]^T 29.6 -> 25.7, x[64, 14336]
-        // W[8192, 14336]^T 56.4 -> 50.8; at K = 4096 the unsplit narrow strips stay faster)
+        // W[8192, 14336]^T 56.4 -> 50.8, x[48, 10240] W[4096, 10240]^T 28.3 -> 23.0; at K =
+        // 8192 the unsplit narrow strips stay faster: x[64, 8192] W[4096, 8192]^T 22.7 vs 24.8)
         Plan q = skinny_nk_plan(r, std::max<int64_t>(2, kNumCUs / wgs64), p.group_m);
         if (q.splits > 1) {
           q.bn = 64;

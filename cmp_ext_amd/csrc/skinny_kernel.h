@@ -253,11 +253,23 @@ __global__ void __launch_bounds__(256) gemm_skinny_nk_kernel(const GemmParams p)
   // Workgroup w (x fastest, then z) runs on XCD w % 8: each XCD takes a contiguous range of
   // (z, strip) in z-major order, so its L2 holds the small operand of one or two batch
   // entries (or K ranges) rather than of all of them.
-  const int64_t wg = blockIdx.x + (int64_t)gridDim.x * blockIdx.z, total = (int64_t)gridDim.x * gridDim.z;
-  const int64_t xcd = wg & 7, base = total >> 3, rem = total & 7;
-  const int64_t order = xcd * base + (xcd < rem ? xcd : rem) + (wg >> 3);
-  const int zz = (int)(order / gridDim.x);
-  const int strip = (int)(order - (int64_t)zz * gridDim.x);
+  // (32-bit arithmetic where the grid allows: a 64-bit division costs every wave ~0.5 us)
+  int zz, strip;
+  const int64_t total = (int64_t)gridDim.x * gridDim.z;
+  if (gridDim.z == 1) {
+    zz = 0;
+    strip = strip_order(blockIdx.x, gridDim.x);
+  } else if (total <= 0x7FFFFFFF) {
+    const uint32_t order = (uint32_t)strip_order(blockIdx.x + gridDim.x * blockIdx.z, (int)total);
+    zz = (int)(order / gridDim.x);
+    strip = (int)(order - (uint32_t)zz * gridDim.x);
+  } else {
+    const int64_t wg = blockIdx.x + (int64_t)gridDim.x * blockIdx.z;
+    const int64_t xcd = wg & 7, base = total >> 3, rem = total & 7;
+    const int64_t order = xcd * base + (xcd < rem ? xcd : rem) + (wg >> 3);
+    zz = (int)(order / gridDim.x);
+    strip = (int)(order - (int64_t)zz * gridDim.x);
+  }
   const int n0 = strip * SW;
   // split K (p.splits > 1): grid.z = batch * splits, split ks sums k in [ks*ksplit, +ksplit)
   // and writes fp32 partials[ks][batch][M][N] (summed, biased and rounded by a second launch)

@@ -271,11 +271,11 @@ def test_skinny_nk_split_k_rule():
         assert (f"splits={expect} " in desc) if expect > 1 else ("splits" not in desc), (M, N, K, desc)
     kid, desc = cabi.plan(cabi.F16, cabi.B_NK, 1, 1024, 14336)
     assert kid == K_SKINNY_NK and "splits" not in desc, desc
-    # more than 16 rows of A and K >= 8192 over <= 128 strips of 64 W rows: those strips, split
-    for M, N, K, expect in [(64, 4096, 14336, 4), (32, 4096, 14336, 4), (64, 8192, 14336, 2), (48, 4096, 8192, 4)]:
+    # more than 16 rows of A and K >= 10240 over <= 128 strips of 64 W rows: those strips, split
+    for M, N, K, expect in [(64, 4096, 14336, 4), (32, 4096, 14336, 4), (64, 8192, 14336, 2), (48, 4096, 10240, 4)]:
         kid, desc = cabi.plan(cabi.F16, cabi.B_NK, M, N, K, workspace_bytes=ws)
         assert kid == K_SKINNY_NK and f"x64 " in desc and f"splits={expect} " in desc, (M, N, K, desc)
-    for M, N, K in [(64, 4096, 4096), (16, 4096, 14336), (64, 14336, 8192)]:
+    for M, N, K in [(64, 4096, 4096), (16, 4096, 14336), (64, 14336, 8192), (64, 4096, 8192)]:
         kid, desc = cabi.plan(cabi.F16, cabi.B_NK, M, N, K, workspace_bytes=ws)
         assert kid == K_SKINNY_NK and "splits" not in desc, (M, N, K, desc)
 
