@@ -138,7 +138,7 @@ namespace {
 struct Override {
   int kernel = -1;
   int splits = 1;
-  int strip = 0;  // tall, skinny_nk: rows of A (of W) per workgroup (16, 32 or 64; 0: the selector's)
+  int strip = 0;  // rows of A (tall: 32 or 64) or of W (skinny_nk: 16, 32 or 64) per workgroup; 0: the selector's
 };
 
 Override read_override() {
@@ -275,7 +275,8 @@ void override16(const Request& r, bool fast, bool stream_ok, bool tall_ok, bool 
       if (o.strip) q.bn = o.strip;
       break;
     case kTall:
-      if (!tall_ok) return;
+      // strips of 32 or 64 rows of A only (0: 64); a 16-row strip is not built for it
+      if (!tall_ok || o.strip == 16) return;
       q = tall_plan(r, o.strip == 32 ? 32 : 64, p->group_m, o.splits);
       break;
     default:

@@ -164,20 +164,21 @@ int cmpext3_gemm_run(const cmpext3_gemm_call* call, void* workspace, int64_t wor
 /*
  * cmpext3_gemm_ex without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc): the call runs exactly the plan
- * cmpext3_gemm_ex would run with all the workspace it asks for, with the
- * library's own static device scratch buffer of CMPEXT3_SCRATCH_BYTES (64 MiB,
- * held by every GPU the library runs on until the process ends) as that
- * workspace.  It calls no allocating routine.  A call whose plan needs more
- * than that (zero-padded copies of large unaligned operands, split-K partials
- * of very large products) returns CMPEXT3_ERR_SCRATCH and launches nothing.
- * The scratch contents need no clearing: every byte a call writes is read back
- * by the same call.  All calls on one GPU share its buffer, so calls that may
- * overlap on one GPU (other streams, other threads) race; order them on one
- * stream.  The first call on a GPU must be made with that GPU current; it looks
- * up the buffer's address there.
- * No counterpart in the reference (its launchers take no workspace at all,
- * src/main.cpp:12-14); it is for callers that cannot allocate.
+ * harnesses that forbid hipMalloc): the call runs the plan cmpext3_gemm_ex
+ * would run with all the workspace it asks for, with the library's own static
+ * device scratch buffer of CMPEXT3_SCRATCH_BYTES (64 MiB, held by every GPU the
+ * library runs on until the process ends) as that workspace.  When that plan
+ * needs more than the scratch holds (zero-padded copies of large unaligned
+ * operands, split-K partials of very large products), it runs the plan
+ * cmpext3_gemm_ex would run with a workspace of CMPEXT3_SCRATCH_BYTES instead
+ * (fewer K splits, or no padded copies); CMPEXT3_ERR_SCRATCH is returned, and
+ * nothing launched, only if even that plan does not fit.  It calls no
+ * allocating routine.  The scratch contents need no clearing: every byte a call
+ * writes is read back by the same call.  All calls on one GPU share its buffer,
+ * so calls that may overlap on one GPU (other streams, other threads) race;
+ * order them on one stream.  The buffer used is that of the stream's GPU (the
+ * current GPU for the null stream); its address is looked up once per GPU.
+ * No counterpart in the reference; it is for callers that cannot allocate.
  */
 #define CMPEXT3_SCRATCH_BYTES (64ll << 20)
 int cmpext3_gemm_ex_noalloc(int dtype, int b_layout,

@@ -317,6 +317,12 @@ def test_gemm_config_override(monkeypatch):
     assert desc.startswith("kernel=tall") and "tile=64x64 grid=2x1x1" in desc and "mb=4" in desc, desc
     assert not cabi.plan(cabi.F16, cabi.B_KN, 1000, 136, 200)[1].startswith("kernel=tall")
     assert not cabi.plan(cabi.F16, cabi.B_KN, 1000, 60, 200)[1].startswith("kernel=tall")
+    # 16-row strips exist for skinny_nk only: a tall override asking for them is ignored
+    # (the selector's own plan), never run as another strip height
+    monkeypatch.delenv("CMPEXT3_GEMM_CONFIG")
+    own = cabi.plan(cabi.BF16, cabi.B_KN, 1000, 72, 200, batch=3)[1]
+    monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=tall,strip=16")
+    assert cabi.plan(cabi.BF16, cabi.B_KN, 1000, 72, 200, batch=3)[1] == own
     # the generic kernel, with no padded copies in its place
     monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=generic64x64")
     desc = cabi.plan(cabi.BF16, cabi.B_KN, 2048, 2048, 2047, workspace_bytes=ws)[1]

@@ -7,8 +7,8 @@ bit, cmpext3_gemm_ex's on a workspace allocated for it (the kernels are
 deterministic and the plans are the same).  Cases cover each user of the
 workspace: split-K fp32 partials of the skinny-M kernel, of the 16-bit tiles
 and of the fp32 tiles, and zero-padded copies of unaligned 16-bit and fp32
-operands; a call that needs more than the scratch holds is refused before
-anything is launched.
+operands; a call whose full plan needs more than the scratch holds runs the
+plan cmpext3_gemm_ex runs with a workspace of the scratch's size.
 """
 import numpy as np
 import pytest
@@ -89,19 +89,49 @@ def test_noalloc_matches_gemm_ex_twice(case):
     assert all(keyword in d for d in descs), descs
 
 
-def test_noalloc_refuses_more_than_the_scratch():
-    # fp16 8191^3 with odd rows: the zero-padded copies of A and B take 2 x 128 MiB
-    M = N = K = 8191
-    a = torch.zeros(M, K, dtype=torch.float16, device="cuda")
-    b = torch.zeros(K, N, dtype=torch.float16, device="cuda")
-    c = torch.full((M, N), 3.0, dtype=torch.float16, device="cuda")
-    st, call = cabi.prepare(cabi.F16, cabi.B_KN, a, K, 0, b, N, 0, c, N, 0, None, M, N, K)
+def test_noalloc_plans_within_the_scratch_when_the_full_plan_needs_more():
+    # fp16 6001^3 with odd rows: the zero-padded copies of A and B would take 2 x 72 MB, so
+    # the call runs the plan cmpext3_gemm_ex runs with a 64 MiB workspace (here: no copies)
+    M = N = K = 6001
+    g = torch.Generator().manual_seed(11)
+    a = (torch.randn(M, K, generator=g) / np.sqrt(K)).to(torch.float16).cuda()
+    b = (torch.randn(K, N, generator=g) / np.sqrt(K)).to(torch.float16).cuda()
+    st, call = cabi.prepare(cabi.F16, cabi.B_KN, a, K, 0, b, N, 0, a, N, 0, None, M, N, K)
     assert st == cabi.OK and cabi.call_workspace_size(call) > cabi.SCRATCH_BYTES
+    st, call = cabi.prepare(cabi.F16, cabi.B_KN, a, K, 0, b, N, 0, a, N, 0, None, M, N, K,
+                            workspace_limit=cabi.SCRATCH_BYTES)
+    assert st == cabi.OK
+    need = cabi.call_workspace_size(call)
+    assert 0 <= need <= cabi.SCRATCH_BYTES
+    ws = torch.empty(cabi.SCRATCH_BYTES, dtype=torch.uint8, device="cuda")
+    c_ref = torch.full((M, N), float("nan"), dtype=torch.float16, device="cuda")
+    st = cabi.gemm_ex(cabi.F16, cabi.B_KN, a, K, 0, b, N, 0, c_ref, N, 0, None, M, N, K, 1, ws)
+    assert st == cabi.OK, cabi.status_string(st)
+    c = torch.full((M, N), float("nan"), dtype=torch.float16, device="cuda")
     st = cabi.gemm_ex_noalloc(cabi.F16, cabi.B_KN, a, K, 0, b, N, 0, c, N, 0, None, M, N, K)
-    assert st == cabi.ERR_SCRATCH
-    assert "scratch" in cabi.status_string(st)
+    assert st == cabi.OK, cabi.status_string(st)
     torch.cuda.synchronize()
-    assert bool((c == 3.0).all())   # nothing was launched
+    assert torch.equal(c, c_ref)
+    rows = [0, 1, 2999, M - 1]
+    ref = O.matmul_f64(O.to_f64(a[rows].cpu()), O.to_f64(b.cpu()))
+    assert O.rel_frobenius(O.to_f64(c[rows].cpu()), ref) <= TOL[cabi.F16]
+
+
+def test_noalloc_on_a_side_stream():
+    # the scratch is that of the stream's GPU; the call is queued on the stream given
+    a, b, _ = operands(cabi.F16, cabi.B_KN, 16, 8192, 8192, 1, 9)
+    c1 = torch.full((16, 8192), float("nan"), dtype=torch.float16, device="cuda")
+    c2 = torch.full_like(c1, float("nan"))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    assert cabi.gemm_ex_noalloc(cabi.F16, cabi.B_KN, a[0], 8192, 0, b[0], 8192, 0, c1, 8192, 0, None,
+                                16, 8192, 8192, stream=side) == cabi.OK
+    side.synchronize()
+    ws = torch.empty(cabi.SCRATCH_BYTES, dtype=torch.uint8, device="cuda")
+    assert cabi.gemm_ex(cabi.F16, cabi.B_KN, a[0], 8192, 0, b[0], 8192, 0, c2, 8192, 0, None,
+                        16, 8192, 8192, 1, ws) == cabi.OK
+    torch.cuda.synchronize()
+    assert torch.equal(c1, c2)
 
 
 def test_noalloc_without_workspace_need_and_bad_arguments():
