@@ -27,7 +27,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
 HIP_SOURCES = [f"tile_{t}_{lay}_{k}.hip" for t in ("f16", "bf16") for lay in ("kn", "nk") for k in ("whole", "ragged")] + \
-    ["skinny.hip", "tall.hip", "stream.hip", "stream_nk.hip", "f32.hip", "generic.hip", "pad.hip", "noalloc.hip"]
+    ["skinny.hip", "tall.hip", "stream.hip", "stream_nk.hip", "f32.hip", "generic.hip", "pad.hip", "noalloc.hip", "sem.hip"]
 HOST_SOURCES = ["selector.cpp", "api.cpp"]
 
 HIP_FLAGS = [

@@ -43,8 +43,13 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
   const BLayout lay = (BLayout)layout;
   switch (plan.kernel) {
     case kSkinnyWide: {
-      hipError_t e = launch_skinny_wide((DType)dtype, plan.mb, p, (float*)ws, plan.splits, plan.ksplit, grid, s);
-      if (e == hipSuccess && plan.splits > 1)
+      // split K: the last workgroup of each column strip to finish sums the partials
+      // (counters of this stream; a batch entry's partial block addressed with 32-bit
+      // byte offsets), else a second launch does
+      const bool fuse = plan.splits > 1 && (int64_t)p.M * p.N * 4 < (1ll << 31);
+      unsigned int* sem = fuse ? split_counters(s, (int64_t)grid.z * (grid.x / plan.splits)) : nullptr;
+      hipError_t e = launch_skinny_wide((DType)dtype, plan.mb, p, (float*)ws, plan.splits, plan.ksplit, grid, s, sem);
+      if (e == hipSuccess && plan.splits > 1 && sem == nullptr)
         e = launch_skinny_reduce((DType)dtype, p, (const float*)ws, plan.splits, (int)grid.z, s);
       return e;
     }

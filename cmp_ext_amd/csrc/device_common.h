@@ -100,9 +100,24 @@ __device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t
   return __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
 }
 // Cache policy of buffer loads and stores that are coherent across the whole
-// device (the sc1 scope bit): a store reaches the memory side instead of staying
-// in the issuing XCD's L2, and a load does not hit a stale line there.
+// device (sc1, the policy the compiler gives relaxed agent-scope atomic loads and
+// stores on gfx950): a store reaches the memory side instead of staying in the
+// issuing XCD's L2, and a load does not hit a stale line there, so no L2
+// write-back or invalidate is needed.  Workgroups that hand partial results to one
+// another use them: the writer waits for its stores to complete (s_waitcnt
+// vmcnt(0)) before it bumps an agent-scope counter, and the reader loads only
+// after that counter has told it the others are done.  `off` is a byte offset
+// from `base` (below 2^31).
 constexpr int kCoherent = 16;
+__device__ __forceinline__ void store16_coherent(float* base, uint32_t off, f32x4 v) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)kBufRecords, kBufWord3);
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kCoherent);
+}
+__device__ __forceinline__ f32x4 load16_coherent(const float* base, uint32_t off) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)kBufRecords, kBufWord3);
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoherent));
+}
 
 // Vector store of 4 bytes; an offset past num_records (kBufOOB) is dropped by
 // the hardware, which is how edge elements are masked without branches.
@@ -290,6 +305,22 @@ __device__ __forceinline__ void tile_coords(int x, int z, int nz, int tiles_m, i
   const int r = t - g * per_group;
   tm = first_m + r % gsz;
   tn = r / gsz;
+}
+
+// ---------------------------------------------------------------------------
+// Host side: launches `kernel` on `s` and returns the status of this launch
+// alone.  (hipGetLastError after a launch would also report, and clear, an
+// earlier failure of unrelated work on the calling thread.)
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Same {
+  using type = T;
+};
+template <typename... P>
+inline hipError_t launch_kernel(void (*kernel)(P...), dim3 grid, dim3 block, size_t shmem, hipStream_t s,
+                                typename Same<P>::type... args) {
+  void* argv[] = {(void*)&args..., nullptr};
+  return hipLaunchKernel((const void*)kernel, grid, block, argv, shmem, s);
 }
 
 }  // namespace cmpext3

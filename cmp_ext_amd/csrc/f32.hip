@@ -9,24 +9,18 @@ template <bool KN, bool SPLITK, bool DMA16>
 hipError_t launch(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s) {
   switch (id) {
     case kF32Tile128:
-      hipLaunchKernelGGL((gemm_f32_kernel<KN, 128, 128, 2, 4, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
-      break;
+      return launch_kernel((gemm_f32_kernel<KN, 128, 128, 2, 4, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
     case kF32Tile96x64:
-      hipLaunchKernelGGL((gemm_f32_kernel<KN, 96, 64, 2, 8, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
-      break;
+      return launch_kernel((gemm_f32_kernel<KN, 96, 64, 2, 8, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
     case kF32Tile64:
-      hipLaunchKernelGGL((gemm_f32_kernel<KN, 64, 64, 2, 8, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
-      break;
+      return launch_kernel((gemm_f32_kernel<KN, 64, 64, 2, 8, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
     case kF32Tile64K4:
-      hipLaunchKernelGGL((gemm_f32_kwave_kernel<64, KN, 2, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
-      break;
+      return launch_kernel((gemm_f32_kwave_kernel<64, KN, 2, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
     case kF32Tile16K4:
-      hipLaunchKernelGGL((gemm_f32_kwave_kernel<16, KN, 2, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
-      break;
+      return launch_kernel((gemm_f32_kwave_kernel<16, KN, 2, SPLITK, DMA16>), grid, dim3(256), 0, s, p);
     default:
       return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 template <bool DMA16>

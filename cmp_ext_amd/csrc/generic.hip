@@ -6,11 +6,8 @@ namespace cmpext3 {
 namespace {
 template <typename T>
 hipError_t launch(BLayout lay, const GemmParams& p, dim3 grid, hipStream_t s) {
-  if (lay == kKN)
-    hipLaunchKernelGGL((gemm_generic_kernel<T, true>), grid, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((gemm_generic_kernel<T, false>), grid, dim3(256), 0, s, p);
-  return hipGetLastError();
+  if (lay == kKN) return launch_kernel((gemm_generic_kernel<T, true>), grid, dim3(256), 0, s, p);
+  return launch_kernel((gemm_generic_kernel<T, false>), grid, dim3(256), 0, s, p);
 }
 }  // namespace
 

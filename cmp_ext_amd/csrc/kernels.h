@@ -22,8 +22,17 @@ hipError_t launch_skinny(DType dt, int mb, const GemmParams& p, dim3 grid, hipSt
 hipError_t launch_skinny_nk(DType dt, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s);
 // N <= 16 * mb: strips of `strip` rows of A over all of K, B as [N, K] or [K, N] (layout)
 hipError_t launch_tall(DType dt, BLayout lay, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s);
+// sem: counters of the in-kernel split reduction (split_counters), or nullptr when the
+// partials are left for launch_skinny_reduce.
 hipError_t launch_skinny_wide(DType dt, int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid,
-                              hipStream_t s);
+                              hipStream_t s, unsigned int* sem);
+// Counters for the split-K reductions done inside the splitting kernel (sem.hip): slots of
+// kSemCounters per stream of a GPU, zero between kernels.  Returns the slot of stream s
+// when `count` counters fit and s is neither capturing a graph nor beyond the first
+// kSemSlots streams of its GPU, else nullptr (the caller then reduces in a second launch).
+constexpr int kSemSlots = 64;
+constexpr int kSemCounters = 4096;
+unsigned int* split_counters(hipStream_t s, int64_t count);
 hipError_t launch_skinny_reduce(DType dt, const GemmParams& p, const float* ws, int splits, int batch,
                                 hipStream_t s);
 // grid.x = 128-column tiles, grid.z = batch entries (one A shared by all, M <= 128); bias none or per row.

@@ -62,15 +62,15 @@ hipError_t launch_pad_copy(const void* src, int64_t src_ld, int64_t src_stride, 
   for (int64_t b0 = 0; b0 < batch; b0 += kMaxZ) {
     const int64_t nb = batch - b0 < kMaxZ ? batch - b0 : kMaxZ;
     const dim3 grid((unsigned)((total + kChunk - 1) / kChunk), 1, (unsigned)nb);
+    hipError_t e;
     if (esz == 2)
-      hipLaunchKernelGGL(pad_copy_kernel<uint16_t>, grid, block, 0, s, (const uint16_t*)src + b0 * src_stride,
+      e = launch_kernel(pad_copy_kernel<uint16_t>, grid, block, 0, s, (const uint16_t*)src + b0 * src_stride,
                          src_ld, src_stride, rows, cols, (uint16_t*)dst + b0 * dst_stride, dst_stride, dst_rows,
                          dst_cols);
     else
-      hipLaunchKernelGGL(pad_copy_kernel<uint32_t>, grid, block, 0, s, (const uint32_t*)src + b0 * src_stride,
+      e = launch_kernel(pad_copy_kernel<uint32_t>, grid, block, 0, s, (const uint32_t*)src + b0 * src_stride,
                          src_ld, src_stride, rows, cols, (uint32_t*)dst + b0 * dst_stride, dst_stride, dst_rows,
                          dst_cols);
-    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

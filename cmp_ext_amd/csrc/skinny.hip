@@ -14,13 +14,12 @@ template <typename T>
 hipError_t launch(int mb, const GemmParams& p, dim3 grid, hipStream_t s) {
   const dim3 block(256);
   switch (mb) {
-    case 1: hipLaunchKernelGGL((gemm_skinny_narrow_kernel<T, 1>), grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL((gemm_skinny_narrow_kernel<T, 2>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((gemm_skinny_narrow_kernel<T, 3>), grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL((gemm_skinny_narrow_kernel<T, 4>), grid, block, 0, s, p); break;
+    case 1: return launch_kernel((gemm_skinny_narrow_kernel<T, 1>), grid, block, 0, s, p);
+    case 2: return launch_kernel((gemm_skinny_narrow_kernel<T, 2>), grid, block, 0, s, p);
+    case 3: return launch_kernel((gemm_skinny_narrow_kernel<T, 3>), grid, block, 0, s, p);
+    case 4: return launch_kernel((gemm_skinny_narrow_kernel<T, 4>), grid, block, 0, s, p);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 }  // namespace
 
@@ -38,16 +37,14 @@ hipError_t launch_nk(int mb, const GemmParams& p, dim3 grid, hipStream_t s) {
   switch (mb) {
     case 1:
       if constexpr (SW == 32)
-        hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 1, 32, 256, NT, 3>), grid, block, 0, s, p);
+        return launch_kernel((gemm_skinny_nk_kernel<T, 1, 32, 256, NT, 3>), grid, block, 0, s, p);
       else
-        hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 1, SW, SW == 64 ? 256 : 512, NT>), grid, block, 0, s, p);
-      break;
-    case 2: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 2, SW, 256, NT>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 3, SW, SW == 64 ? 128 : 256, NT>), grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, SW, SW == 64 ? 128 : 256, NT>), grid, block, 0, s, p); break;
+        return launch_kernel((gemm_skinny_nk_kernel<T, 1, SW, SW == 64 ? 256 : 512, NT>), grid, block, 0, s, p);
+    case 2: return launch_kernel((gemm_skinny_nk_kernel<T, 2, SW, 256, NT>), grid, block, 0, s, p);
+    case 3: return launch_kernel((gemm_skinny_nk_kernel<T, 3, SW, SW == 64 ? 128 : 256, NT>), grid, block, 0, s, p);
+    case 4: return launch_kernel((gemm_skinny_nk_kernel<T, 4, SW, SW == 64 ? 128 : 256, NT>), grid, block, 0, s, p);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 template <typename T>
 hipError_t launch_nk(int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {
@@ -66,43 +63,44 @@ hipError_t launch_skinny(DType dt, int mb, const GemmParams& p, dim3 grid, hipSt
 
 namespace {
 template <typename T, bool NT>
-hipError_t launch_wide(int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid, hipStream_t s) {
+hipError_t launch_wide(int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid, hipStream_t s,
+                       unsigned int* sem) {
   const dim3 block(256);
   switch (mb) {
-    case 1: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 1, NT>), grid, block, 0, s, p, ws, splits, ksplit); break;
-    case 2: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 2, NT>), grid, block, 0, s, p, ws, splits, ksplit); break;
-    case 3: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 3, NT>), grid, block, 0, s, p, ws, splits, ksplit); break;
-    case 4: hipLaunchKernelGGL((gemm_skinny_wide_kernel<T, 4, NT>), grid, block, 0, s, p, ws, splits, ksplit); break;
+    case 1: return launch_kernel((gemm_skinny_wide_kernel<T, 1, NT>), grid, block, 0, s, p, ws, splits, ksplit, sem);
+    case 2: return launch_kernel((gemm_skinny_wide_kernel<T, 2, NT>), grid, block, 0, s, p, ws, splits, ksplit, sem);
+    case 3: return launch_kernel((gemm_skinny_wide_kernel<T, 3, NT>), grid, block, 0, s, p, ws, splits, ksplit, sem);
+    case 4: return launch_kernel((gemm_skinny_wide_kernel<T, 4, NT>), grid, block, 0, s, p, ws, splits, ksplit, sem);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 template <typename T>
-hipError_t launch_wide(int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid, hipStream_t s) {
-  return stream_once(p.K, p.N, p.stride_b, grid.z) ? launch_wide<T, true>(mb, p, ws, splits, ksplit, grid, s)
-                                                   : launch_wide<T, false>(mb, p, ws, splits, ksplit, grid, s);
+hipError_t launch_wide(int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid, hipStream_t s,
+                       unsigned int* sem) {
+  return stream_once(p.K, p.N, p.stride_b, grid.z) ? launch_wide<T, true>(mb, p, ws, splits, ksplit, grid, s, sem)
+                                                   : launch_wide<T, false>(mb, p, ws, splits, ksplit, grid, s, sem);
 }
 }  // namespace
 
 hipError_t launch_skinny_wide(DType dt, int mb, const GemmParams& p, float* ws, int splits, int ksplit, dim3 grid,
-                              hipStream_t s) {
-  if (dt == kF16) return launch_wide<_Float16>(mb, p, ws, splits, ksplit, grid, s);
-  if (dt == kBF16) return launch_wide<__bf16>(mb, p, ws, splits, ksplit, grid, s);
+                              hipStream_t s, unsigned int* sem) {
+  if (splits <= 1) sem = nullptr;
+  if (dt == kF16) return launch_wide<_Float16>(mb, p, ws, splits, ksplit, grid, s, sem);
+  if (dt == kBF16) return launch_wide<__bf16>(mb, p, ws, splits, ksplit, grid, s, sem);
   return hipErrorInvalidValue;
 }
 
 namespace {
 template <typename T, int V>
-void launch_reduce(const GemmParams& p, const float* ws, int splits, int batch, int vec, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((skinny_reduce_kernel<T, V>), grid, dim3(256), 0, s, p, ws, splits, batch, vec);
+hipError_t launch_reduce(const GemmParams& p, const float* ws, int splits, int batch, int vec, dim3 grid,
+                         hipStream_t s) {
+  return launch_kernel((skinny_reduce_kernel<T, V>), grid, dim3(256), 0, s, p, ws, splits, batch, vec);
 }
 template <typename T>
-void launch_reduce(int V, const GemmParams& p, const float* ws, int splits, int batch, int vec, dim3 grid,
-                   hipStream_t s) {
-  if (V == 8)
-    launch_reduce<T, 8>(p, ws, splits, batch, vec, grid, s);
-  else
-    launch_reduce<T, 4>(p, ws, splits, batch, vec, grid, s);
+hipError_t launch_reduce(int V, const GemmParams& p, const float* ws, int splits, int batch, int vec, dim3 grid,
+                         hipStream_t s) {
+  if (V == 8) return launch_reduce<T, 8>(p, ws, splits, batch, vec, grid, s);
+  return launch_reduce<T, 4>(p, ws, splits, batch, vec, grid, s);
 }
 }  // namespace
 
@@ -124,13 +122,9 @@ hipError_t launch_skinny_reduce(DType dt, const GemmParams& p, const float* ws, 
   // one V-column chunk per thread; past 65536 workgroups the threads loop (grid stride)
   const int64_t chunks = rows * (p.N / V);
   const dim3 grid((unsigned)std::min<int64_t>((chunks + 255) / 256, 65536));
-  if (dt == kF16)
-    launch_reduce<_Float16>(V, p, ws, splits, batch, vec, grid, s);
-  else if (dt == kBF16)
-    launch_reduce<__bf16>(V, p, ws, splits, batch, vec, grid, s);
-  else
-    launch_reduce<float>(V, p, ws, splits, batch, vec, grid, s);
-  return hipGetLastError();
+  if (dt == kF16) return launch_reduce<_Float16>(V, p, ws, splits, batch, vec, grid, s);
+  if (dt == kBF16) return launch_reduce<__bf16>(V, p, ws, splits, batch, vec, grid, s);
+  return launch_reduce<float>(V, p, ws, splits, batch, vec, grid, s);
 }
 hipError_t launch_skinny_nk(DType dt, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {
   if (dt == kF16) return launch_nk<_Float16>(mb, strip, p, grid, s);

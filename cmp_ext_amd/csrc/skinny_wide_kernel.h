@@ -13,8 +13,12 @@
 //     [k][n] tile, A fragments from ds_read_b128 (v_mfma_f32_16x16x32, the M
 //     rows in the MFMA's 16-wide dimension);
 //   * with S == 1 writes C directly; otherwise writes its fp32 partial block
-//     to the workspace, and skinny_reduce_kernel sums the S partials, adds the
-//     bias and rounds to the output type.
+//     to the workspace and counts itself in on its strip's counter (`sem`);
+//     the last of the strip's S workgroups to arrive sums the S partials in
+//     split order, adds the bias, rounds to the output type, writes C and
+//     resets the counter.  Without counters (sem == nullptr)
+//     skinny_reduce_kernel does that sum in a second launch, with the same
+//     arithmetic (bit-identical results).
 #pragma once
 
 #include <type_traits>
@@ -55,7 +59,7 @@ __device__ __forceinline__ uint32_t wide_off(int k, int seg) {
 // for the next call).
 template <typename T, int MB, bool NT = false>
 __global__ void __launch_bounds__(256) gemm_skinny_wide_kernel(const GemmParams p, float* ws, int splits,
-                                                               int ksplit) {
+                                                               int ksplit, unsigned int* sem) {
   using S = WideShape<MB>;
   constexpr int NS = S::NS;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * S::STAGE];
@@ -187,11 +191,65 @@ __global__ void __launch_bounds__(256) gemm_skinny_wide_kernel(const GemmParams 
           crow[n + r] = to_bits<T>(x);
         }
       } else {
-        float* w = ws + (((int64_t)split * gridDim.z + bz) * M + m) * N + n;
-        *(f32x4*)w = acc[h][mb];
+        float* blk = ws + ((int64_t)split * gridDim.z + bz) * M * N;  // this (split, batch entry) block
+        if (sem != nullptr)
+          store16_coherent(blk, (uint32_t)(m * N + n) * 4u, acc[h][mb]);
+        else
+          *(f32x4*)(blk + m * N + n) = acc[h][mb];
       }
     }
   }
+  if (splits == 1 || sem == nullptr) return;
+
+  // ---- the strip's split reduction, by the last of its workgroups to arrive ----
+  // The partials went out as GPU-coherent stores (store16_coherent); every wave waits
+  // for them to complete, then one thread counts the workgroup in with an agent-scope
+  // atomic.  The last to arrive reads the others' partials with GPU-coherent loads.
+  // (Agent-scope release/acquire fences would instead write back and invalidate the
+  // XCD's whole L2 per workgroup: measured on MI355X, 16 x 8192 x 8192 took 34.7 us
+  // with one such fence pair per workgroup against ~28 us for two launches.)
+  __shared__ int last;
+  unsigned int* count = sem + bz * (gridDim.x / splits) + strip;
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+  __syncthreads();
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (unsigned int)(splits - 1);
+  __syncthreads();
+  if (!last) return;
+  const int cols = min(kWideStrip, N - n0);  // a multiple of 8
+  for (int idx = tid; idx < M * (kWideStrip / 4); idx += 256) {
+    const int m = idx / (kWideStrip / 4), n = n0 + 4 * (idx % (kWideStrip / 4));
+    if (n - n0 >= cols) continue;
+    // sum in split order from zero, then the bias, then one rounding: the arithmetic of
+    // skinny_reduce_kernel
+    f32x4 acc4 = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < splits; s0 += 8) {  // up to 8 loads in flight, then the adds in order
+      f32x4 part[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < splits)
+          part[j] = load16_coherent(ws + ((s0 + j) * gridDim.z + bz) * M * N, (uint32_t)(m * N + n) * 4u);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < splits) acc4 += part[j];
+    }
+    uint16_t* crow = (uint16_t*)((T*)p.C + bz * p.stride_c + (int64_t)m * p.ldc) + n;
+    uint16_t h[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float x = acc4[r];
+      if (bias) x += from_bits<T>(bias[p.bias_row ? m : n + r]);
+      h[r] = to_bits<T>(x);
+    }
+    if (((uintptr_t)crow & 7) == 0) {
+      *(u32x2*)crow = u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) crow[r] = h[r];
+    }
+  }
+  if (tid == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next kernel
 }
 
 // C = sum over the S partial blocks in the workspace (+ bias), rounded to T.

@@ -22,8 +22,7 @@ hipError_t launch_stream(DType dt, BLayout lay, const GemmParams& p, dim3 grid, 
   if (per_block >= 8) per_block -= per_block % 8;
   const unsigned wgs = (unsigned)(per_block * row_blocks);
   if (lay == kNK) return launch_stream_nk(dt, p, (int)total, wgs, s);
-  launch_stream_layout<false>(dt, p, (int)total, wgs, s);
-  return hipGetLastError();
+  return launch_stream_layout<false>(dt, p, (int)total, wgs, s);
 }
 
 }  // namespace cmpext3

@@ -5,8 +5,7 @@
 namespace cmpext3 {
 
 hipError_t launch_stream_nk(DType dt, const GemmParams& p, int total, unsigned wgs, hipStream_t s) {
-  launch_stream_layout<true>(dt, p, total, wgs, s);
-  return hipGetLastError();
+  return launch_stream_layout<true>(dt, p, total, wgs, s);
 }
 
 }  // namespace cmpext3

@@ -18,24 +18,22 @@ template <typename T, bool XKN, bool NT>
 hipError_t launch_tall_t(int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {
   const dim3 block(256);
   if (mb == 4 && strip == 32)
-    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, 32, 256, NT, 3, true, XKN>), grid, block, 0, s, p);
-  else if (mb == 4 && strip == 64)
-    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 4, 64, 128, NT, 8, true, XKN>), grid, block, 0, s, p);
-  else if (!XKN && mb == 1 && strip == 32)
-    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 1, 32, 256, NT, 3, true, false>), grid, block, 0, s, p);
-  else if (!XKN && mb == 1 && strip == 64)
-    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 1, 64, 256, NT, 8, true, false>), grid, block, 0, s, p);
-  else if (!XKN && mb == 2 && strip == 32)
-    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 2, 32, 256, NT, 3, true, false>), grid, block, 0, s, p);
-  else if (!XKN && mb == 2 && strip == 64)
-    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 2, 64, 256, NT, 8, true, false>), grid, block, 0, s, p);
-  else if (mb == 8 && strip == 32)
-    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 8, 32, 128, NT, 8, true, XKN>), grid, block, 0, s, p);
-  else if (mb == 8 && strip == 64)
-    hipLaunchKernelGGL((gemm_skinny_nk_kernel<T, 8, 64, 128, NT, 8, true, XKN>), grid, block, 0, s, p);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+    return launch_kernel((gemm_skinny_nk_kernel<T, 4, 32, 256, NT, 3, true, XKN>), grid, block, 0, s, p);
+  if (mb == 4 && strip == 64)
+    return launch_kernel((gemm_skinny_nk_kernel<T, 4, 64, 128, NT, 8, true, XKN>), grid, block, 0, s, p);
+  if (!XKN && mb == 1 && strip == 32)
+    return launch_kernel((gemm_skinny_nk_kernel<T, 1, 32, 256, NT, 3, true, false>), grid, block, 0, s, p);
+  if (!XKN && mb == 1 && strip == 64)
+    return launch_kernel((gemm_skinny_nk_kernel<T, 1, 64, 256, NT, 8, true, false>), grid, block, 0, s, p);
+  if (!XKN && mb == 2 && strip == 32)
+    return launch_kernel((gemm_skinny_nk_kernel<T, 2, 32, 256, NT, 3, true, false>), grid, block, 0, s, p);
+  if (!XKN && mb == 2 && strip == 64)
+    return launch_kernel((gemm_skinny_nk_kernel<T, 2, 64, 256, NT, 8, true, false>), grid, block, 0, s, p);
+  if (mb == 8 && strip == 32)
+    return launch_kernel((gemm_skinny_nk_kernel<T, 8, 32, 128, NT, 8, true, XKN>), grid, block, 0, s, p);
+  if (mb == 8 && strip == 64)
+    return launch_kernel((gemm_skinny_nk_kernel<T, 8, 64, 128, NT, 8, true, XKN>), grid, block, 0, s, p);
+  return hipErrorInvalidValue;
 }
 template <typename T>
 hipError_t launch_tall_t(BLayout lay, int mb, int strip, const GemmParams& p, dim3 grid, hipStream_t s) {

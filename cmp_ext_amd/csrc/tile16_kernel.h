@@ -404,20 +404,17 @@ __global__ void __launch_bounds__(64 * WM * WN, MINB) gemm_tile16_kernel(const G
 // Launches gemm_tile16_kernel (WM x WN waves, MINB workgroups per CU) with the
 // bias mode and the K split the arguments ask for.
 template <typename T, bool KN, int BM, int BN, int WM, int WN, int MINB, bool KCHECK>
-void launch_tile16_k(const GemmParams& p, dim3 grid, hipStream_t s) {
+hipError_t launch_tile16_k(const GemmParams& p, dim3 grid, hipStream_t s) {
   const dim3 block(64 * WM * WN);
   if constexpr (BM >= 128) {
-    if (p.splits > 1) {  // fp32 partials; the bias comes with the reduction
-      hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 0, MINB, true, KCHECK>), grid, block, 0, s, p);
-      return;
-    }
+    if (p.splits > 1)  // fp32 partials; the bias comes with the reduction
+      return launch_kernel((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 0, MINB, true, KCHECK>), grid, block, 0, s, p);
   }
   if (p.bias == nullptr)
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 0, MINB, false, KCHECK>), grid, block, 0, s, p);
-  else if (p.bias_row)
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 2, MINB, false, KCHECK>), grid, block, 0, s, p);
-  else
-    hipLaunchKernelGGL((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 1, MINB, false, KCHECK>), grid, block, 0, s, p);
+    return launch_kernel((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 0, MINB, false, KCHECK>), grid, block, 0, s, p);
+  if (p.bias_row)
+    return launch_kernel((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 2, MINB, false, KCHECK>), grid, block, 0, s, p);
+  return launch_kernel((gemm_tile16_kernel<T, KN, BM, BN, WM, WN, 1, MINB, false, KCHECK>), grid, block, 0, s, p);
 }
 
 }  // namespace cmpext3

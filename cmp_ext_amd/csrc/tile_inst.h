@@ -14,21 +14,16 @@ template <typename T, bool KN, bool KCHECK>
 hipError_t launch_tiles(KernelId id, const GemmParams& p, dim3 grid, hipStream_t s) {
   switch (id) {
     case kTile256x256:
-      launch_tile16_k<T, KN, 256, 256, 4, 2, 1, KCHECK>(p, grid, s);
-      break;
+      return launch_tile16_k<T, KN, 256, 256, 4, 2, 1, KCHECK>(p, grid, s);
     case kTile256x224:
-      launch_tile16_k<T, KN, 256, 224, 4, 2, 1, KCHECK>(p, grid, s);
-      break;
+      return launch_tile16_k<T, KN, 256, 224, 4, 2, 1, KCHECK>(p, grid, s);
     case kTile128x128:
-      launch_tile16_k<T, KN, 128, 128, 2, 2, 2, KCHECK>(p, grid, s);
-      break;
+      return launch_tile16_k<T, KN, 128, 128, 2, 2, 2, KCHECK>(p, grid, s);
     case kTile64x256:
-      launch_tile16_k<T, KN, 64, 256, 1, 4, 2, KCHECK>(p, grid, s);
-      break;
+      return launch_tile16_k<T, KN, 64, 256, 1, 4, 2, KCHECK>(p, grid, s);
     default:
       return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace cmpext3
