@@ -16,23 +16,39 @@ HBM3E 8 TB/s).  `traffic` (HBM bytes per launch) comes from the committed
 rocprofv3 FETCH_SIZE/WRITE_SIZE summary in profiles/hbm_traffic.json when it
 has an entry for the workload, else null.
 
-cpu_baseline (every config): the reference CPU path that BASELINE.json names --
-the same op via torch.matmul on CPU tensors in the config's dtype
-(oracle.gemm_oracle.cpu_matmul), timed on this host's cores on two row samples
-of the workload (about 8 s each), both reported with their rate ratio and the
-host's CPU model, thread count and ISA.
+Inputs: every workload's operands are drawn before any timing starts, by a CPU
+torch.Generator seeded with 0 (A first, then B, in float32, then cast to the
+dtype), and copied to the GPU -- the same values the float64 oracle checks
+(oracle.gemm_oracle.make_inputs draws them the same way).
 
-power: board power and shader clock (amdsmi gpu_metrics) read while the timed
-steps of each workload ran; MFMA-bound rooflines also carry the fraction of the
-matrix peak at that clock (`frac_at_measured_sclk`; the nominal `frac` is the
-record).  torch_same_device: the same op through torch on the same GPU, timed the
-same way, as the reference's own harness compares (context, not the measured path).
+cpu_baseline (every workload): the reference CPU path that BASELINE.json names --
+the same op via torch on CPU tensors in the workload's dtype
+(oracle.gemm_oracle.cpu_matmul for the configs), timed on this host's cores on
+two samples of the workload (whole rows of A, or whole images), each call at
+least ~0.3 s, both reported with their rate ratio and the host's CPU model,
+thread count and ISA.  When the two rates differ by more than 0.8..1.25 the
+rate is not a property of the op at that size: `value` is then null and
+`null_reason` says so.
 
-callers: the three reference callers on the GEMM path, at the shapes of the
-reference's own benchmark (tools/bench.py:156-200): linear with bias, bmm and a
-1x1 conv2d, each timed like the configs, with its roofline and the same op on
-CPU tensors (torch) timed beside it on two bounded samples (about 3 s each).
-`python bench.py --caller NAME` times one of them alone (for profiling).
+power: after every workload's timed steps, the same op runs back to back for
+--power-window seconds (default 1) while board power and shader clock (amdsmi
+gpu_metrics) are read; MFMA-bound rooflines also carry the fraction of the
+matrix peak at that sustained clock (`frac_at_sustained_sclk`; the nominal
+`frac` is the record).  torch_same_device: the same op through torch on the
+same GPU, timed the same way, as the reference's own harness compares
+(context, not the measured path).
+
+callers: the reference callers on the GEMM path, at the shapes of the
+reference's own benchmark (tools/bench.py:156-200), in the dtypes its suites
+run (tools/bench.py:538-556): linear with bias and bmm in fp16, bf16 and fp32,
+and a 1x1 conv2d in fp16, each timed like the configs, with its roofline and
+the same op on CPU tensors (torch) timed beside it.  `python bench.py --caller
+NAME` times one of them alone (for profiling).
+
+Kernel traces: each timed region is bracketed, outside its two HIP events, by a
+one-element int64 fill (a torch FillFunctor<long> kernel), and stderr names the
+regions in order ("bench: timed region i: ..."), so that the dispatches of the
+timed calls can be picked out of a rocprofv3 kernel trace of this command.
 """
 from __future__ import annotations
 
@@ -59,7 +75,9 @@ CONFIGS = {
     "cfg4_fp16_skinny": dict(dtype="fp16", M=16, N=8192, K=8192, dist="normal", scale=8192 ** -0.5,
                              desc="fp16_matmul 16x8192 @ 8192x8192 (decode, HBM-bound)", hbm=True),
     "cfg5_fp32_ragged": dict(dtype="fp32", M=4097, N=3001, K=2049, dist="uniform",
-                             desc="fp32_matmul 4097x2049 @ 2049x3001 (ragged)"),
+                             desc="fp32_matmul 4097x2049 @ 2049x3001 (ragged)",
+                             provenance="the reference's only fp32 GEMM figure is '5.6T' (~5.6 TFLOP/s, GA100-tuned, "
+                                        "shape and device not stated; src/cuda/fp32_matmul.cu:288): not a vs_baseline"),
 }
 HEADLINE = "cfg2_fp16_4096"
 # Order in which the workloads are timed (the headline, wherever it appears, last unless
@@ -70,15 +88,28 @@ HEADLINE = "cfg2_fp16_4096"
 # warm-up calls its timed steps include part of that ramp.  The order does not change this
 # (measured: timing the matrix-core-bound workloads right after each other moved no figure
 # by more than the run-to-run spread).
-ORDER = ["cfg4_fp16_skinny", "cfg5_fp32_ragged", "linear_fp16_4096", "bmm_fp16_16x1024",
-         "conv1x1_fp16_64x128x128x128", "cfg3_bf16_mlp", "cfg2_fp16_4096"]
+ORDER = ["cfg4_fp16_skinny", "cfg5_fp32_ragged", "linear_fp32_4096", "bmm_fp32_16x1024", "linear_fp16_4096",
+         "linear_bf16_4096", "bmm_fp16_16x1024", "bmm_bf16_16x1024", "conv1x1_fp16_64x128x128x128",
+         "cfg3_bf16_mlp", "cfg2_fp16_4096"]
 
-# The reference callers at the reference benchmark's shapes (fp16, its first suite).
+# The reference callers at the reference benchmark's shapes, in the dtypes of its suites
+# (tools/bench.py:538-556 runs FP32, FP16 and BF16).
 CALLERS = {
     "linear_fp16_4096": dict(op="linear", dtype="fp16", M=4096, N=4096, K=4096, batch=1,
                              desc="cmpext3.linear: x[4096,4096] @ W[4096,4096]^T + b (tools/bench.py:156-174)"),
+    "linear_bf16_4096": dict(op="linear", dtype="bf16", M=4096, N=4096, K=4096, batch=1,
+                             desc="cmpext3.linear bf16: x[4096,4096] @ W[4096,4096]^T + b (tools/bench.py:156-174)",
+                             provenance="the reference's only published bf16 figure is this call: 6.723 ms "
+                                        "(~20.4 TFLOP/s), 150 W on an NVIDIA CMP 170HX (src/cuda/bf16_matmul.cu:318); "
+                                        "other hardware, so not a vs_baseline"),
+    "linear_fp32_4096": dict(op="linear", dtype="fp32", M=4096, N=4096, K=4096, batch=1,
+                             desc="cmpext3.linear fp32: x[4096,4096] @ W[4096,4096]^T + b (tools/bench.py:156-174)"),
     "bmm_fp16_16x1024": dict(op="bmm", dtype="fp16", M=1024, N=1024, K=1024, batch=16,
                              desc="cmpext3.bmm: [16,1024,1024] @ [16,1024,1024] (tools/bench.py:177-179)"),
+    "bmm_bf16_16x1024": dict(op="bmm", dtype="bf16", M=1024, N=1024, K=1024, batch=16,
+                             desc="cmpext3.bmm bf16: [16,1024,1024] @ [16,1024,1024] (tools/bench.py:177-179)"),
+    "bmm_fp32_16x1024": dict(op="bmm", dtype="fp32", M=1024, N=1024, K=1024, batch=16,
+                             desc="cmpext3.bmm fp32: [16,1024,1024] @ [16,1024,1024] (tools/bench.py:177-179)"),
     "conv1x1_fp16_64x128x128x128": dict(op="conv", dtype="fp16", M=64, N=128 * 128, K=128, batch=64, hbm=True,
                                         desc="cmpext3.conv2d 1x1 with bias: input [64,128,128,128] -> 64 "
                                              "channels (the tensors of tools/bench.py:197-200 at kernel size 1)"),
@@ -219,15 +250,32 @@ def power_clock() -> PowerClock:
 POWER_WINDOW_S = 1.0
 
 
-def timed_region(fn, steps: int, warmup: int) -> tuple[float, float]:
+_MARK = []
+
+
+def trace_mark() -> None:
+    """A one-element int64 fill (torch's FillFunctor<long> kernel): the bracket of a
+    timed region in a kernel trace.  Always outside the region's events and wall clock."""
+    import torch
+
+    if not _MARK:
+        _MARK.append(torch.empty(1, dtype=torch.int64, device="cuda"))
+    _MARK[0].fill_(len(_MARK))
+
+
+def timed_region(fn, steps: int, warmup: int, label: str = "") -> tuple[float, float]:
     """W untimed calls, then K calls between two events on the current stream
     (the stream the kernels run on), bracketed by synchronizations.  Returns
-    (wall ms per step, event ms per step)."""
+    (wall ms per step, event ms per step).  A trace marker goes out after the
+    warm-up calls and after the timed calls, and stderr names the region."""
     import torch
 
     stream = torch.cuda.current_stream()
     for i in range(warmup):
         fn(i)
+    log(f"timed region {len(TIMED_REGIONS)}: {label} ({warmup} warm-up calls, then {steps} timed)")
+    TIMED_REGIONS.append(label)
+    trace_mark()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -237,7 +285,11 @@ def timed_region(fn, steps: int, warmup: int) -> tuple[float, float]:
     e1.record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    trace_mark()
     return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
+
+
+TIMED_REGIONS: list = []
 
 
 def power_window(fn, kern_ms: float, window_s: float) -> dict:
@@ -269,20 +321,47 @@ def power_window(fn, kern_ms: float, window_s: float) -> dict:
     return pc.summary(samples, time.perf_counter() - w0)
 
 
-def make_gpu_inputs(c, nb: int, seed: int = 0):
+def make_cpu_inputs(c, nb: int, seed: int = 0):
+    """A config's operands as BASELINE.json draws them: a CPU torch.Generator seeded
+    with `seed` draws A, then B, in float32 (uniform[-1, 1] or normal(0, 1) * scale),
+    each cast to the dtype; `nb` - 1 more B buffers follow from the same generator."""
     import torch
 
     dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[c["dtype"]]
-    g = torch.Generator(device="cuda").manual_seed(seed)
+    g = torch.Generator().manual_seed(seed)
 
     def draw(shape):
         if c["dist"] == "uniform":
-            return (torch.rand(shape, generator=g, device="cuda") * 2 - 1).to(dt)
-        return (torch.randn(shape, generator=g, device="cuda") * c["scale"]).to(dt)
+            return (torch.rand(shape, generator=g, dtype=torch.float32) * 2 - 1).to(dt)
+        return (torch.randn(shape, generator=g, dtype=torch.float32) * c["scale"]).to(dt)
 
     a = draw((c["M"], c["K"]))
     bs = [draw((c["K"], c["N"])) for _ in range(nb)]
     return a, bs
+
+
+# Device-resident operands of every workload to be timed, drawn before any timing.
+INPUTS: dict = {}
+
+
+def b_buffers(c) -> int:
+    # The skinny config streams all of B; its 128 MiB would stay in the 256 MB Infinity
+    # Cache across calls, so it cycles through 4 distinct B buffers.
+    return 4 if c.get("hbm") else 1
+
+
+def prepare_inputs(names) -> None:
+    for name in names:
+        if name in INPUTS:
+            continue
+        if name in CONFIGS:
+            a, bs = make_cpu_inputs(CONFIGS[name], b_buffers(CONFIGS[name]))
+            INPUTS[name] = (a.cuda(), [b.cuda() for b in bs])
+        else:
+            INPUTS[name] = tuple(x.cuda() for x in caller_inputs(CALLERS[name]))
+    import torch
+
+    torch.cuda.synchronize()
 
 
 def time_gpu(name: str, steps: int, warmup: int, with_torch: bool = True) -> dict:
@@ -292,11 +371,10 @@ def time_gpu(name: str, steps: int, warmup: int, with_torch: bool = True) -> dic
 
     c = CONFIGS[name]
     fn = {"fp16": cmpext3.fp16_matmul, "bf16": cmpext3.bf16_matmul, "fp32": cmpext3.fp32_matmul}[c["dtype"]]
-    # The skinny config streams all of B; its 128 MiB would stay in the 256 MB
-    # Infinity Cache across calls, so it cycles through 4 distinct B buffers.
-    nb = 4 if c.get("hbm") else 1
-    a, bs = make_gpu_inputs(c, nb)
-    wall_ms, kern_ms = timed_region(lambda i: fn(a, bs[i % nb]), steps, warmup)
+    prepare_inputs([name])
+    a, bs = INPUTS[name]
+    nb = len(bs)
+    wall_ms, kern_ms = timed_region(lambda i: fn(a, bs[i % nb]), steps, warmup, name)
     plan = cmpext3.last_plan()
     flops, nbytes = algorithmic(c)
     r = dict(config=name, desc=c["desc"], dtype=c["dtype"], kernel=plan.split()[0].split("=")[1], plan=plan,
@@ -304,7 +382,8 @@ def time_gpu(name: str, steps: int, warmup: int, with_torch: bool = True) -> dic
              tflops=flops / (wall_ms * 1e-3) / 1e12, kernel_tflops=flops / (kern_ms * 1e-3) / 1e12,
              gbs=nbytes / (wall_ms * 1e-3) / 1e9, kernel_gbs=nbytes / (kern_ms * 1e-3) / 1e9)
     if with_torch:
-        t = torch_same_device(torch.matmul, lambda i: (a, bs[i % nb]), steps, warmup, flops, nbytes, c.get("hbm"))
+        t = torch_same_device(torch.matmul, lambda i: (a, bs[i % nb]), steps, warmup, flops, nbytes, c.get("hbm"),
+                              name + " (torch)")
         t["speedup"] = round(t["kernel_ms"] / kern_ms, 3)
         r["torch_same_device"] = t
     # run later (power_window), after every workload's timed steps; keeps the inputs alive
@@ -326,15 +405,16 @@ def caller_algorithmic(c) -> tuple[float, float]:
     return flops, float(nbytes)
 
 
-def caller_inputs(c, device: str, seed: int = 0):
-    """Seeded inputs of a caller, fp16 (scaled so that outputs stay O(1))."""
+def caller_inputs(c, seed: int = 0):
+    """Seeded CPU inputs of a caller in its dtype (normal, scaled so that outputs stay
+    O(1)), drawn by a CPU torch.Generator in float32 in argument order."""
     import torch
 
     dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[c["dtype"]]
-    g = torch.Generator(device=device).manual_seed(seed)
+    g = torch.Generator().manual_seed(seed)
 
     def draw(shape, scale):
-        return (torch.randn(shape, generator=g, device=device) * scale).to(dt)
+        return (torch.randn(shape, generator=g, dtype=torch.float32) * scale).to(dt)
 
     Bn, M, N, K = c["batch"], c["M"], c["N"], c["K"]
     if c["op"] == "linear":
@@ -360,23 +440,25 @@ def time_caller(name: str, steps: int, warmup: int, with_torch: bool = True) -> 
     import cmpext3
 
     c = CALLERS[name]
-    args = caller_inputs(c, "cuda")
+    prepare_inputs([name])
+    args = INPUTS[name]
     fn = caller_fn(c, cmpext3)
-    wall_ms, kern_ms = timed_region(lambda i: fn(*args), steps, warmup)
+    wall_ms, kern_ms = timed_region(lambda i: fn(*args), steps, warmup, name)
     flops, nbytes = caller_algorithmic(c)
     plan = cmpext3.last_plan()
     kernel = plan.split()[0].split("=")[1]
     ref = None
     if with_torch:
         tfn = {"linear": F.linear, "bmm": torch.bmm, "conv": F.conv2d}[c["op"]]
-        ref = torch_same_device(tfn, lambda i: args, steps, warmup, flops, nbytes, c.get("hbm"))
+        ref = torch_same_device(tfn, lambda i: args, steps, warmup, flops, nbytes, c.get("hbm"), name + " (torch)")
         ref["speedup"] = round(ref["kernel_ms"] / kern_ms, 3)
     if c.get("hbm"):
         ach, peak, unit, bound = nbytes / (kern_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s", "hbm"
     else:
         ach, peak, unit, bound = flops / (kern_ms * 1e-3) / 1e12, PEAK[c["dtype"]], "TFLOP/s", "mfma"
     val = nbytes / (wall_ms * 1e-3) / 1e9 if c.get("hbm") else flops / (wall_ms * 1e-3) / 1e12
-    return {"desc": c["desc"], "kernel": kernel, "plan": plan, "ms_per_step": round(wall_ms, 5),
+    return {"desc": c["desc"], **({"provenance": c["provenance"]} if "provenance" in c else {}),
+            "kernel": kernel, "plan": plan, "ms_per_step": round(wall_ms, 5),
             unit: round(val, 2),
             "roofline": {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
                          "frac": round(ach / peak, 4), "traffic": load_traffic(name), "kernel": kernel,
@@ -408,15 +490,13 @@ def cpu_description() -> str:
             f"ISA: {' '.join(isa) or 'none of avx512f/avx512_bf16/avx512_fp16/amx'}")
 
 
-def sample_rate(run, limit: int, budget_s: float, start: int = 8, probe_s: float = 0.2,
-                sizes: tuple[int, int] | None = None, min_calls: int = 2) -> dict:
-    """Times `run(n)` (work on the first n rows of a workload; returns its work in the
-    metric's unit) on two sample sizes: n grows by 4x from `start` until a call takes
-    `probe_s` or n reaches `limit`, then the last two sizes (or n/2 and n) are each
-    repeated for about budget_s / 2 (at least twice, counting the probe).  Returns the
-    median rate of each size, so that the assumption that the rate per row does not
-    depend on the sample size can be checked.  `sizes` fixes the two sizes instead
-    (no probing), each timed at least `min_calls` times."""
+def sample_rate(run, limit: int, budget_s: float, probe_s: float = 0.5, whole: bool = False) -> dict:
+    """Times `run(n)` (the op on the first n units of a workload -- rows of A, or whole
+    images; returns its work in the metric's unit).  With `whole`, the whole workload
+    (n = limit) is timed.  Otherwise n doubles from 1 until a call takes `probe_s` or n
+    reaches `limit`, and n / 2 and n are each timed for about budget_s / 2 (at least two
+    calls each), so that the rate's independence of the sample size can be checked.
+    Returns {n: (work, median seconds per call, calls)}."""
     timing = {}
 
     def once(n):
@@ -427,56 +507,58 @@ def sample_rate(run, limit: int, budget_s: float, start: int = 8, probe_s: float
         return dt
 
     run(1)  # warm-up (first-call overheads)
-    if sizes is None:
-        n = min(start, limit)
-        probed = []
-        while True:
-            dt = once(n)
-            probed.append(n)
-            if dt >= probe_s or n >= limit:
-                break
-            n = min(limit, 4 * n)
-        if len(probed) == 1 and n > 1:
-            probed = [max(1, n // 2), n]
-        pair = probed[-2:]
+    if whole:
+        pair = [limit]
     else:
-        pair = list(sizes)
+        n = 1
+        while once(n) < probe_s and n < limit:
+            n = min(limit, 2 * n)
+        pair = [max(1, n // 2), n] if n > 1 else [1]
     for m in pair:
         t_start = time.perf_counter()
-        while len(timing.get(m, [0, []])[1]) < min_calls or (time.perf_counter() - t_start < budget_s / 2
-                                                            and len(timing[m][1]) < 20):
+        while len(timing.get(m, [0, []])[1]) < 2 or (time.perf_counter() - t_start < budget_s / len(pair)
+                                                      and len(timing[m][1]) < 20):
             once(m)
     return {m: (timing[m][0], statistics.median(timing[m][1]), len(timing[m][1])) for m in pair}
 
 
-def rate_summary(rates: dict, unit: str, what: str) -> dict:
-    """cpu_baseline object from sample_rate's two sizes: the value of the larger sample,
-    both samples listed, and the ratio of their rates (1.0 = proportional)."""
-    (n1, (w1, t1, c1)), (n2, (w2, t2, c2)) = sorted(rates.items())[0], sorted(rates.items())[-1]
-    r1, r2 = w1 / t1, w2 / t2
+def rate_summary(rates: dict, unit: str, what: str, units: str = "rows") -> dict:
+    """cpu_baseline object from sample_rate: the rate of the larger sample when the two
+    samples' rates agree within 0.8..1.25 (else value null, with the reason), both
+    samples listed; a whole-workload timing needs no such check."""
     import torch
 
-    return {"value": round(r2, 6), "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{what}, rows 0..{n2 - 1}; median of {c2} calls ({t2 * 1e3:.1f} ms/call)",
-            "samples": [{"rows": n1, "ms_per_call": round(t1 * 1e3, 2), "value": round(r1, 6), "calls": c1},
-                        {"rows": n2, "ms_per_call": round(t2 * 1e3, 2), "value": round(r2, 6), "calls": c2}],
-            "rate_ratio_large_over_small": round(r2 / r1, 3) if r1 > 0 else None,
-            "host": cpu_description()}
+    items = sorted(rates.items())
+    n2, (w2, t2, c2) = items[-1]
+    r2 = w2 / t2
+    out = {"value": round(r2, 6), "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+           "sample": f"{what}: {units} 0..{n2 - 1}; median of {c2} calls ({t2 * 1e3:.1f} ms/call)",
+           "samples": [{units: n, "ms_per_call": round(t * 1e3, 2), "value": round(w / t, 6), "calls": c}
+                       for n, (w, t, c) in items]}
+    if len(items) > 1:
+        n1, (w1, t1, c1) = items[0]
+        ratio = r2 / (w1 / t1)
+        out["rate_ratio_large_over_small"] = round(ratio, 3)
+        if not 0.8 <= ratio <= 1.25:
+            out["value"] = None
+            out["null_reason"] = (f"the rates of {n1} and {n2} {units} differ by {ratio:.2f}x: the CPU rate "
+                                  "depends on the sample size here, so no sample rate stands for the workload")
+    out["host"] = cpu_description()
+    return out
 
 
-def cpu_caller(name: str, budget_s: float = 3.0) -> dict:
+def cpu_caller(name: str, budget_s: float = 6.0) -> dict:
     """The same caller on CPU tensors (torch.nn.functional.linear, torch.bmm,
-    torch.nn.functional.conv2d) on two bounded samples: the first n rows of x
-    (linear), of batch entry 0's A (bmm) or of image 0 (conv)."""
+    torch.nn.functional.conv2d): rows of x (linear), rows of batch entry 0's A (bmm),
+    or whole images (conv)."""
     import torch
     import torch.nn.functional as F
 
     c = CALLERS[name]
-    args = caller_inputs(c, "cpu")
+    args = caller_inputs(c)
     M, N, K = c["M"], c["N"], c["K"]
-    hw = int(round(N ** 0.5))
-    limit = {"linear": M, "bmm": M, "conv": hw}[c["op"]]
-    hbm = c.get("hbm")
+    limit = {"linear": M, "bmm": M, "conv": c["batch"]}[c["op"]]
+    esz = 4 if c["dtype"] == "fp32" else 2
 
     def run(n):
         if c["op"] == "linear":
@@ -485,21 +567,23 @@ def cpu_caller(name: str, budget_s: float = 3.0) -> dict:
         if c["op"] == "bmm":
             torch.bmm(args[0][:1, :n], args[1][:1])
             return 2.0 * n * N * K / 1e12
-        F.conv2d(args[0][:1, :, :n], args[1], args[2])
-        # bytes of the sample: its input rows, output rows, weight and bias (GB)
-        return 2.0 * (n * hw * K + n * hw * M + M * K + M) / 1e9 if hbm else 2.0 * n * hw * M * K / 1e12
+        F.conv2d(args[0][:n], args[1], args[2])
+        # bytes of the sample: its images in and out, the weight and the bias (GB)
+        return esz * (n * N * K + n * N * M + M * K + M) / 1e9
 
     what = {"linear": f"F.linear on CPU ({c['dtype']}): x rows @ the full W^T + b",
             "bmm": f"torch.bmm on CPU ({c['dtype']}): rows of batch entry 0 @ its full B",
-            "conv": f"F.conv2d 1x1 on CPU ({c['dtype']}): image rows of image 0"}[c["op"]]
-    return rate_summary(sample_rate(run, limit, budget_s), "GB/s" if hbm else "TFLOP/s", what)
+            "conv": f"F.conv2d 1x1 on CPU ({c['dtype']}): whole images"}[c["op"]]
+    log(f"cpu baseline {name}")
+    return rate_summary(sample_rate(run, limit, budget_s), "GB/s" if c.get("hbm") else "TFLOP/s", what,
+                        "images" if c["op"] == "conv" else "rows")
 
 
-def cpu_baseline(name: str, budget_s: float = 8.0) -> dict:
+def cpu_baseline(name: str, budget_s: float = 6.0) -> dict:
     """The reference CPU path that BASELINE.json names -- torch.matmul on CPU tensors in
-    the config's dtype (oracle.gemm_oracle.cpu_matmul) -- on two row samples of the
-    same workload (the first n rows of A times all of B).  For the HBM-bound config
-    the value is GB/s of the sample's own bytes (its rows of A and C, all of B)."""
+    the config's dtype (oracle.gemm_oracle.cpu_matmul) -- on rows of A times all of B.
+    The HBM-bound config is timed whole (all of B is read for any rows, so a row
+    sample's GB/s is not the workload's)."""
     import torch  # noqa: F401
 
     from oracle.gemm_oracle import cpu_matmul, make_inputs
@@ -516,19 +600,17 @@ def cpu_baseline(name: str, budget_s: float = 8.0) -> dict:
         return 2.0 * n * c["N"] * c["K"] / 1e12
 
     log(f"cpu baseline {name}")
-    # GB/s of a row sample is not that of the whole (all of B is read for any rows): the
-    # HBM-bound config (M = 16) is timed whole, beside its first half
-    rates = sample_rate(run, c["M"], budget_s, sizes=(c["M"] // 2, c["M"]) if hbm else None,
-                        min_calls=1 if hbm else 2)
+    rates = sample_rate(run, c["M"], budget_s, whole=bool(hbm))
     return rate_summary(rates, "GB/s" if hbm else "TFLOP/s",
                         f"torch.matmul on CPU ({c['dtype']}) of A rows @ the full B ({c['K']}x{c['N']}) of {name}")
 
 
-def torch_same_device(fn, args_fn, steps: int, warmup: int, flops: float, nbytes: float, hbm: bool) -> dict:
+def torch_same_device(fn, args_fn, steps: int, warmup: int, flops: float, nbytes: float, hbm: bool,
+                      label: str = "torch") -> dict:
     """The same op through torch on the same GPU (hipBLASLt / MIOpen), timed like ours
     -- the reference harness's comparison (tools/bench.py:67-104, speedup at :172).
     Context only: never part of the measured path."""
-    wall_ms, kern_ms = timed_region(lambda i: fn(*args_fn(i)), steps, warmup)
+    wall_ms, kern_ms = timed_region(lambda i: fn(*args_fn(i)), steps, warmup, label)
     out = {"ms_per_step": round(wall_ms, 5), "kernel_ms": round(kern_ms, 5)}
     if hbm:
         out["GB/s"] = round(nbytes / (kern_ms * 1e-3) / 1e9, 1)
@@ -665,6 +747,16 @@ def main() -> int:
         log(f"{args.config}: {r['ms_per_step']:.4f} ms/step, {r['tflops']:.1f} TFLOP/s, {r['gbs']:.0f} GB/s")
         return r
 
+    # every workload's operands are drawn (CPU generator) and copied to the GPU first, so
+    # that no timed region follows an idle GPU waiting on the host's random draws
+    order = [n for n in args.order.split(",") if n]
+    unknown = [n for n in order if n not in CONFIGS and n not in CALLERS]
+    if unknown:
+        raise SystemExit(f"bench.py: unknown workloads in --order: {unknown}")
+    todo = [args.config] if args.no_others else \
+        [n for n in order if n != args.config and not (n in CALLERS and args.no_callers)] + [args.config]
+    log(f"drawing the inputs of {len(todo)} workloads")
+    prepare_inputs(todo)
     head = headline() if args.headline_first or args.no_others else None
     others = {}
 
@@ -678,7 +770,8 @@ def main() -> int:
         r = time_gpu(name, args.steps, args.warmup, with_torch)
         log(f"{name}: {r['ms_per_step']:.4f} ms/step, {r['tflops']:.1f} TFLOP/s, {r['gbs']:.0f} GB/s")
         c = CONFIGS[name]
-        others[name] = {"desc": r["desc"], "kernel": r["kernel"], "plan": r["plan"],
+        others[name] = {"desc": r["desc"], **({"provenance": c["provenance"]} if "provenance" in c else {}),
+                        "kernel": r["kernel"], "plan": r["plan"],
                         "ms_per_step": round(r["ms_per_step"], 5),
                         **({"GB/s": round(r["gbs"], 1)} if c.get("hbm") else
                            {"TFLOP/s": round(r["tflops"], 2)}),
@@ -688,10 +781,6 @@ def main() -> int:
 
     callers = {}
     if not args.no_others:
-        order = [n for n in args.order.split(",") if n]
-        unknown = [n for n in order if n not in CONFIGS and n not in CALLERS]
-        if unknown:
-            raise SystemExit(f"bench.py: unknown workloads in --order: {unknown}")
         for name in order:
             if name == args.config or (name in CALLERS and args.no_callers):
                 continue
@@ -714,7 +803,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": {"fp16": "f16", "bf16": "bf16", "fp32": "f32"}[c["dtype"]],
-        "data": "synthetic (seeded torch.randn / torch.rand on the GPU, BASELINE.json distributions)",
+        "data": "synthetic (a CPU torch.Generator seeded with 0 draws A, then B, in BASELINE.json's "
+                "distributions; cast to the dtype and copied to the GPU before any timing)",
         "config": {"workload": f"{args.config}: {c['desc']}", "M": c["M"], "N": c["N"], "K": c["K"],
                    "accumulate": "fp32", "kernel": head["kernel"], "plan": head["plan"]},
         "roofline": roofline(head, args.config),
@@ -742,7 +832,6 @@ def main() -> int:
     if callers:
         if not args.no_cpu:
             for name in callers:
-                log(f"cpu baseline {name}")
                 callers[name]["cpu_baseline"] = cpu_caller(name)
         line["callers"] = callers
     print(json.dumps(line), flush=True)
