@@ -80,16 +80,17 @@ CONFIGS = {
                                         "shape and device not stated; src/cuda/fp32_matmul.cu:288): not a vs_baseline"),
 }
 HEADLINE = "cfg2_fp16_4096"
-# Order in which the workloads are timed (the headline, wherever it appears, last unless
-# --headline-first).  A matrix-core-bound workload runs slower for its first ~20 ms of
-# calls while the shader clock settles under the power limit (MI355X, bf16 4096 x 14336 x
-# 4096 after 0.2 s idle: medians of successive groups of 20 calls 416, 377, 352, 342, then
-# 340 us; 358 us for the first group right after 40 ms of fp16 4096^3 calls), so with few
-# warm-up calls its timed steps include part of that ramp.  The order does not change this
-# (measured: timing the matrix-core-bound workloads right after each other moved no figure
-# by more than the run-to-run spread).
-ORDER = ["cfg4_fp16_skinny", "cfg5_fp32_ragged", "linear_fp32_4096", "bmm_fp32_16x1024", "linear_fp16_4096",
-         "linear_bf16_4096", "bmm_fp16_16x1024", "bmm_bf16_16x1024", "conv1x1_fp16_64x128x128x128",
+# Order in which the workloads are timed (the headline last).  A matrix-core-bound
+# workload that follows an idle or HBM-bound stretch runs slower for its first tens of ms
+# while the board's power management settles (MI355X, fp32 4097 x 3001 x 2049 right
+# after the HBM-bound skinny config: successive calls 549, 449, 475, 508, 496 .. then
+# 390 us after a second; bf16 4096 x 14336 x 4096 after the 1x1 convolution: 366 .. 387,
+# then 330 us), so with few warm-up calls the timed steps would sit in that transient.
+# The HBM-bound workloads go first, then the fp32 ones, then the 16-bit ones, each
+# group from the least to the most sensitive, so that every matrix-core-bound workload
+# follows another of its kind.
+ORDER = ["cfg4_fp16_skinny", "conv1x1_fp16_64x128x128x128", "linear_fp32_4096", "bmm_fp32_16x1024",
+         "cfg5_fp32_ragged", "linear_fp16_4096", "linear_bf16_4096", "bmm_fp16_16x1024", "bmm_bf16_16x1024",
          "cfg3_bf16_mlp", "cfg2_fp16_4096"]
 
 # The reference callers at the reference benchmark's shapes, in the dtypes of its suites

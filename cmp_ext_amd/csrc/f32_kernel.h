@@ -20,10 +20,13 @@
 // NS-2 stages of loads are always in flight without staging registers.
 //
 // LDS layouts (per stage):
-//   A, and B given as [N,K]: [row][k], rows of 16 floats (64 bytes), 16-byte
-//     chunk c of row r stored at chunk c ^ ((r/4)%4) (f32_off): a fragment
-//     read (16 consecutive rows at one chunk, ds_read_b128) is conflict free,
-//     and one DMA instruction writes 4 whole rows.
+//   A, and B given as [N,K]: rows of 16 floats (64 bytes) in groups of 16 rows
+//     (1 KiB); the 16-byte chunk c (k = 4c..4c+3) of row r sits at slot
+//     f32_slot(r % 16, c) of its group, a layout measured free of LDS bank
+//     conflicts for the fragment read (16 consecutive rows at one chunk per 16
+//     lanes, ds_read_b128).  A DMA instruction writes a quarter of a group
+//     (4-byte DMA) or a whole group (16-byte DMA), each lane fetching the
+//     element f32_slot_src names for its slot.
 //   B given as [K,N]: [k][n], rows of BN floats, 16-float segment s of row k
 //     stored at segment s ^ ((k/4)%4): the fragment read of MFMA step s
 //     (rows s, 4+s, 8+s, 12+s at 16 columns, ds_read_b32) hits 64 distinct
@@ -58,9 +61,27 @@ struct F32Shape {
   static_assert(NS * STAGE <= 160 * 1024, "LDS");
 };
 
-// Byte offset of 16-byte chunk `chunk` (0..3) of row `row` in a [row][16 floats] block.
+// 16-byte slot (0..63) of chunk c (0..3) of row r (0..15) in its 1 KiB group of 16 rows:
+// with bits r0..r3 of r and c0, c1 of c, slot bits are r1^c0^c1, r0^r1^r3, r0^r3, r0,
+// r2, r2^c1.  Found by sweeping GF(2)-linear layouts of the group on MI355X with the LDS
+// bank-conflict counter (SQ_LDS_BANK_CONFLICT): for the fragment read (lane l reads chunk
+// l / 16 of row l % 16, ds_read_b128) this one measured zero conflict cycles at every
+// LDS base offset tried, where the earlier chunk ^ (r / 4) % 4 swizzle (four rows per 256
+// bytes) took one extra cycle per read, as did a third of the layouts swept.
+__device__ __forceinline__ int f32_slot(int r, int c) {
+  const int r0 = r & 1, r1 = (r >> 1) & 1, r2 = (r >> 2) & 1, r3 = (r >> 3) & 1, c0 = c & 1, c1 = (c >> 1) & 1;
+  return (r1 ^ c0 ^ c1) | ((r0 ^ r1 ^ r3) << 1) | ((r0 ^ r3) << 2) | (r0 << 3) | (r2 << 4) | ((r2 ^ c1) << 5);
+}
+// The row (0..15) and chunk whose data slot s of a group holds (the inverse of f32_slot).
+__device__ __forceinline__ void f32_slot_src(int s, int& r, int& c) {
+  const int s0 = s & 1, s1 = (s >> 1) & 1, s2 = (s >> 2) & 1, s3 = (s >> 3) & 1, s4 = (s >> 4) & 1, s5 = (s >> 5) & 1;
+  const int r0 = s3, r1 = s1 ^ s2, r2 = s4, r3 = s2 ^ s3, c1 = s4 ^ s5, c0 = s0 ^ r1 ^ c1;
+  r = r0 | (r1 << 1) | (r2 << 2) | (r3 << 3);
+  c = c0 | (c1 << 1);
+}
+// Byte offset of 16-byte chunk `chunk` (0..3) of row `row` in a block of rows of 16 floats.
 __device__ __forceinline__ uint32_t f32_off(int row, int chunk) {
-  return (uint32_t)((row >> 2) * 256 + 16 * (4 * (row & 3) + (chunk ^ ((row >> 2) & 3))));
+  return (uint32_t)((row >> 4) * 1024 + 16 * f32_slot(row & 15, chunk));
 }
 
 // WAVES: waves per SIMD the kernel is compiled for (caps its registers at 512 / WAVES).
@@ -96,16 +117,17 @@ __global__ void __launch_bounds__(256, WAVES) gemm_f32_kernel(const GemmParams p
                           : (const float*)p.B + bz * p.stride_b + (int64_t)n0 * ldb + kbeg;
 
   // ---- DMA sources: the inverse of the LDS layouts, relative to the stage's k0 ----
-  // [row][k] blocks: instruction t writes rows 4t..4t+3; lane l lands in row
-  // 4t + l/16 at chunk slot (l/4)%4, element l%4, which holds data chunk
-  // slot ^ (t%4).
+  // Row blocks: 4-byte instruction t writes slots 16 (t % 4) .. +15 of group t / 4, lane l
+  // element l % 4 of slot 16 (t % 4) + l / 4.
   uint32_t a_off[S::A_DMA];
   int a_k[S::A_DMA];
 #pragma unroll
   for (int i = 0; i < S::A_DMA; ++i) {
     const int t = wave * S::A_DMA + i;
-    const int row = 4 * t + (lane >> 4);
-    const int k = 4 * (((lane >> 2) & 3) ^ (t & 3)) + (lane & 3);
+    int r, c;
+    f32_slot_src(16 * (t & 3) + (lane >> 2), r, c);
+    const int row = 16 * (t >> 2) + r;
+    const int k = 4 * c + (lane & 3);
     a_off[i] = (m0 + row < M) ? (uint32_t)(row * lda + k) * 4u : kBufOOB;
     a_k[i] = k;
   }
@@ -125,22 +147,26 @@ __global__ void __launch_bounds__(256, WAVES) gemm_f32_kernel(const GemmParams p
       b_off[i] = (n0 + n < N) ? (uint32_t)(k * ldb + n) * 4u : kBufOOB;
       b_k[i] = k;
     } else {
-      const int row = 4 * t + (lane >> 4);
-      const int k = 4 * (((lane >> 2) & 3) ^ (t & 3)) + (lane & 3);
+      int r, c;
+      f32_slot_src(16 * (t & 3) + (lane >> 2), r, c);
+      const int row = 16 * (t >> 2) + r;
+      const int k = 4 * c + (lane & 3);
       b_off[i] = (n0 + row < N) ? (uint32_t)(row * ldb + k) * 4u : kBufOOB;
       b_k[i] = k;
     }
   }
-  // DMA16 sources: A (and B as [N,K]) instruction t writes rows 16t .. 16t+15, lane l
-  // landing in row 16t + l/4 at chunk slot l%4, which holds data chunk slot ^ ((row/4)%4);
-  // B as [K,N]: instruction t writes floats 256t + 4l .. +3 of the stage's [16][BN] block.
+  // DMA16 sources: A (and B as [N,K]) instruction t writes group t (rows 16t .. 16t+15),
+  // lane l slot l; B as [K,N]: instruction t writes floats 256t + 4l .. +3 of the stage's
+  // [16][BN] block.
   uint32_t va_off[S::A16], vb_off[S::B16];
   int va_k[S::A16], vb_k[S::B16];
   if constexpr (DMA16) {
 #pragma unroll
     for (int i = 0; i < S::A16; ++i) {
-      const int row = 16 * (4 * i + wave) + (lane >> 2);
-      const int k = 4 * ((lane & 3) ^ ((row >> 2) & 3));
+      int r, c;
+      f32_slot_src(lane, r, c);
+      const int row = 16 * (4 * i + wave) + r;
+      const int k = 4 * c;
       va_off[i] = (m0 + row < M) ? (uint32_t)(row * lda + k) * 4u : kBufOOB;
       va_k[i] = k;
     }
@@ -153,8 +179,10 @@ __global__ void __launch_bounds__(256, WAVES) gemm_f32_kernel(const GemmParams p
         vb_off[i] = (n0 + n < N) ? (uint32_t)(k * ldb + n) * 4u : kBufOOB;
         vb_k[i] = k;
       } else {
-        const int row = 16 * (4 * i + wave) + (lane >> 2);
-        const int k = 4 * ((lane & 3) ^ ((row >> 2) & 3));
+        int r, c;
+        f32_slot_src(lane, r, c);
+        const int row = 16 * (4 * i + wave) + r;
+        const int k = 4 * c;
         vb_off[i] = (n0 + row < N) ? (uint32_t)(row * ldb + k) * 4u : kBufOOB;
         vb_k[i] = k;
       }

@@ -58,17 +58,22 @@ __global__ void __launch_bounds__(256, BM == 16 ? 4 : 2) gemm_f32_kwave_kernel(c
                           : (const float*)p.B + bz * p.stride_b + (int64_t)n0 * ldb + kbeg;
 
   // ---- DMA sources of one step (the inverse of the LDS layouts), relative to its k0 ----
-  // 4-byte: A (and B as [N,K]) instruction t writes rows 4t..4t+3, lane l landing in row
-  // 4t + l/16 at chunk slot (l/4)%4, element l%4, which holds data chunk slot ^ (t%4);
-  // B as [K,N]: instruction t writes row k = t, lane l in segment slot l/16 holding data
-  // segment slot ^ ((k/4)%4).  16-byte: rows 16t..16t+15, lane l in row 16t + l/4 at chunk
-  // slot l%4 (data chunk slot ^ ((row/4)%4)); B as [K,N]: floats 256t + 4l .. +3.
+  // Row blocks (f32_off): 4-byte instruction t writes slots 16 (t % 4) .. +15 of group
+  // t / 4, lane l element l % 4 of slot 16 (t % 4) + l / 4; 16-byte instruction t writes
+  // group t, lane l slot l.  B as [K,N]: 4-byte instruction t writes row k = t, lane l in
+  // segment slot l/16 holding data segment slot ^ ((k/4)%4); 16-byte: floats 256t + 4l .. +3.
   uint32_t a_off[NA], b_off[NB];
   int a_k[NA], b_k[NB];
+  auto row_piece = [&](int t, int& row, int& k) {
+    int r, c;
+    f32_slot_src(DMA16 ? lane : 16 * (t & 3) + (lane >> 2), r, c);
+    row = DMA16 ? 16 * t + r : 16 * (t >> 2) + r;
+    k = DMA16 ? 4 * c : 4 * c + (lane & 3);
+  };
 #pragma unroll
   for (int t = 0; t < NA; ++t) {
-    const int row = DMA16 ? 16 * t + (lane >> 2) : 4 * t + (lane >> 4);
-    const int k = DMA16 ? 4 * ((lane & 3) ^ ((row >> 2) & 3)) : 4 * (((lane >> 2) & 3) ^ (t & 3)) + (lane & 3);
+    int row, k;
+    row_piece(t, row, k);
     a_off[t] = (m0 + row < M) ? (uint32_t)(row * lda + k) * 4u : kBufOOB;
     a_k[t] = k;
   }
@@ -87,8 +92,8 @@ __global__ void __launch_bounds__(256, BM == 16 ? 4 : 2) gemm_f32_kwave_kernel(c
       b_off[t] = (n0 + n < N) ? (uint32_t)(k * ldb + n) * 4u : kBufOOB;
       b_k[t] = k;
     } else {
-      const int row = DMA16 ? 16 * t + (lane >> 2) : 4 * t + (lane >> 4);
-      const int k = DMA16 ? 4 * ((lane & 3) ^ ((row >> 2) & 3)) : 4 * (((lane >> 2) & 3) ^ (t & 3)) + (lane & 3);
+      int row, k;
+      row_piece(t, row, k);
       b_off[t] = (n0 + row < N) ? (uint32_t)(row * ldb + k) * 4u : kBufOOB;
       b_k[t] = k;
     }
