@@ -9,10 +9,13 @@ configurations (bf16 MLP up-projection, fp16 M=16 skinny, ragged fp32) timed
 the same way.  Rank 0 prints ONE JSON line.
 
 roofline: algorithmic FLOP (2*M*N*K) or bytes (A + B + C once) per launch of
-the dominant kernel, divided by its average duration measured with HIP events
-on the stream the kernel runs on (PyTorch's current stream), against MI355X's
-published peaks (dense fp16/bf16 MFMA 2516.6 TFLOP/s, fp32 MFMA 157.3 TFLOP/s,
-HBM3E 8 TB/s).  `traffic` (HBM bytes per launch) comes from the committed
+the dominant kernel, divided by its average duration back to back (`kernel_ms`:
+HIP events on the stream the kernel runs on, PyTorch's current stream, after
+the first and after the last timed call, so over calls 2..K: the GPU waits from
+the region's first event until the host has enqueued the first call, which is
+host latency, not kernel time; `event_ms_per_step` is the same over all K calls
+from an event before the first), against MI355X's published peaks (dense
+fp16/bf16 MFMA 2516.6 TFLOP/s, fp32 MFMA 157.3 TFLOP/s, HBM3E 8 TB/s).  `traffic` (HBM bytes per launch) comes from the committed
 rocprofv3 FETCH_SIZE/WRITE_SIZE summary in profiles/hbm_traffic.json when it
 has an entry for the workload, else null.
 
@@ -264,11 +267,15 @@ def trace_mark() -> None:
     _MARK[0].fill_(len(_MARK))
 
 
-def timed_region(fn, steps: int, warmup: int, label: str = "") -> tuple[float, float]:
-    """W untimed calls, then K calls between two events on the current stream
-    (the stream the kernels run on), bracketed by synchronizations.  Returns
-    (wall ms per step, event ms per step).  A trace marker goes out after the
-    warm-up calls and after the timed calls, and stderr names the region."""
+def timed_region(fn, steps: int, warmup: int, label: str = "") -> tuple[float, float, float]:
+    """W untimed calls, then K calls bracketed by synchronizations, with HIP events on
+    the current stream (the stream the kernels run on) before the first, after the
+    first and after the last timed call.  Returns (wall ms per step over the K calls,
+    event ms per step over the K calls, event ms per call over calls 2..K).  The last
+    is the kernel's back-to-back duration: the GPU idles from the first event until
+    the host has enqueued the first call (tens of us after a synchronization), which
+    the other two include.  A trace marker goes out after the warm-up calls and after
+    the timed calls, and stderr names the region."""
     import torch
 
     stream = torch.cuda.current_stream()
@@ -278,16 +285,19 @@ def timed_region(fn, steps: int, warmup: int, label: str = "") -> tuple[float, f
     TIMED_REGIONS.append(label)
     trace_mark()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0, e_first, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
     t0 = time.perf_counter()
     e0.record(stream)
     for i in range(steps):
         fn(i)
+        if i == 0:
+            e_first.record(stream)
     e1.record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     trace_mark()
-    return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
+    steady = e_first.elapsed_time(e1) / (steps - 1) if steps > 1 else e0.elapsed_time(e1)
+    return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps, steady
 
 
 TIMED_REGIONS: list = []
@@ -375,11 +385,11 @@ def time_gpu(name: str, steps: int, warmup: int, with_torch: bool = True) -> dic
     prepare_inputs([name])
     a, bs = INPUTS[name]
     nb = len(bs)
-    wall_ms, kern_ms = timed_region(lambda i: fn(a, bs[i % nb]), steps, warmup, name)
+    wall_ms, event_ms, kern_ms = timed_region(lambda i: fn(a, bs[i % nb]), steps, warmup, name)
     plan = cmpext3.last_plan()
     flops, nbytes = algorithmic(c)
     r = dict(config=name, desc=c["desc"], dtype=c["dtype"], kernel=plan.split()[0].split("=")[1], plan=plan,
-             power=None, ms_per_step=wall_ms, kernel_ms=kern_ms,
+             power=None, ms_per_step=wall_ms, kernel_ms=kern_ms, event_ms_per_step=event_ms,
              tflops=flops / (wall_ms * 1e-3) / 1e12, kernel_tflops=flops / (kern_ms * 1e-3) / 1e12,
              gbs=nbytes / (wall_ms * 1e-3) / 1e9, kernel_gbs=nbytes / (kern_ms * 1e-3) / 1e9)
     if with_torch:
@@ -444,7 +454,7 @@ def time_caller(name: str, steps: int, warmup: int, with_torch: bool = True) -> 
     prepare_inputs([name])
     args = INPUTS[name]
     fn = caller_fn(c, cmpext3)
-    wall_ms, kern_ms = timed_region(lambda i: fn(*args), steps, warmup, name)
+    wall_ms, event_ms, kern_ms = timed_region(lambda i: fn(*args), steps, warmup, name)
     flops, nbytes = caller_algorithmic(c)
     plan = cmpext3.last_plan()
     kernel = plan.split()[0].split("=")[1]
@@ -463,7 +473,7 @@ def time_caller(name: str, steps: int, warmup: int, with_torch: bool = True) -> 
             unit: round(val, 2),
             "roofline": {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
                          "frac": round(ach / peak, 4), "traffic": load_traffic(name), "kernel": kernel,
-                         "kernel_ms": round(kern_ms, 5)},
+                         "kernel_ms": round(kern_ms, 5), "event_ms_per_step": round(event_ms, 5)},
             "power": None, **({"torch_same_device": ref} if ref else {}),
             "power_job": lambda window_s: power_window(lambda i: fn(*args), kern_ms, window_s)}
 
@@ -611,7 +621,7 @@ def torch_same_device(fn, args_fn, steps: int, warmup: int, flops: float, nbytes
     """The same op through torch on the same GPU (hipBLASLt / MIOpen), timed like ours
     -- the reference harness's comparison (tools/bench.py:67-104, speedup at :172).
     Context only: never part of the measured path."""
-    wall_ms, kern_ms = timed_region(lambda i: fn(*args_fn(i)), steps, warmup, label)
+    wall_ms, _, kern_ms = timed_region(lambda i: fn(*args_fn(i)), steps, warmup, label)
     out = {"ms_per_step": round(wall_ms, 5), "kernel_ms": round(kern_ms, 5)}
     if hbm:
         out["GB/s"] = round(nbytes / (kern_ms * 1e-3) / 1e9, 1)
@@ -649,7 +659,7 @@ def roofline(r: dict, name: str) -> dict:
         ach, peak, unit, bound = r["kernel_tflops"], PEAK[c["dtype"]], "TFLOP/s", "mfma"
     return {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
             "frac": round(ach / peak, 4), "traffic": load_traffic(name), "kernel": r["kernel"],
-            "kernel_ms": round(r["kernel_ms"], 5)}
+            "kernel_ms": round(r["kernel_ms"], 5), "event_ms_per_step": round(r["event_ms_per_step"], 5)}
 
 
 def main() -> int:
