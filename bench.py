@@ -505,8 +505,9 @@ def sample_rate(run, limit: int, budget_s: float, probe_s: float = 0.5, whole: b
     """Times `run(n)` (the op on the first n units of a workload -- rows of A, or whole
     images; returns its work in the metric's unit).  With `whole`, the whole workload
     (n = limit) is timed.  Otherwise n doubles from 1 until a call takes `probe_s` or n
-    reaches `limit`, and n / 2 and n are each timed for about budget_s / 2 (at least two
-    calls each), so that the rate's independence of the sample size can be checked.
+    reaches `limit`, and n / 2 and n (1 and 2 if one unit already takes `probe_s`) are
+    each timed for about budget_s / 2 (at least two calls each), so that the rate's
+    independence of the sample size can be checked.
     Returns {n: (work, median seconds per call, calls)}."""
     timing = {}
 
@@ -524,7 +525,8 @@ def sample_rate(run, limit: int, budget_s: float, probe_s: float = 0.5, whole: b
         n = 1
         while once(n) < probe_s and n < limit:
             n = min(limit, 2 * n)
-        pair = [max(1, n // 2), n] if n > 1 else [1]
+        # two sizes even when one unit already takes probe_s (e.g. one whole image)
+        pair = [max(1, n // 2), n] if n > 1 else ([1, 2] if limit >= 2 else [1])
     for m in pair:
         t_start = time.perf_counter()
         while len(timing.get(m, [0, []])[1]) < 2 or (time.perf_counter() - t_start < budget_s / len(pair)
