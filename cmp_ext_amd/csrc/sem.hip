@@ -9,9 +9,10 @@
 // split into slots of kSemCounters counters; a slot belongs to one stream of
 // one GPU (the first kSemSlots streams of a GPU to ask get one each, in
 // order), because kernels of one stream never overlap while kernels of two
-// streams may.  Calls on a further stream, or under graph capture (whose
-// kernels may later replay on any stream), get no slot: they reduce in a
-// second launch instead.
+// streams may.  Calls on a further stream, on hipStreamPerThread (one handle for
+// a different stream per host thread), or under graph capture (whose kernels
+// may later replay on any stream), get no slot: they reduce in a second launch
+// instead.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -40,7 +41,8 @@ Table g_tab[kMaxDevices];
 }  // namespace
 
 unsigned int* split_counters(hipStream_t s, int64_t count) {
-  if (count <= 0 || count > kSemCounters) return nullptr;
+  // hipStreamPerThread names a different stream on every host thread: no slot can be its own
+  if (count <= 0 || count > kSemCounters || s == hipStreamPerThread) return nullptr;
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
   int dev = -1;

@@ -129,3 +129,39 @@ def test_more_streams_than_counter_slots():
         for h in streams:
             hip.hipStreamSynchronize(h)
             hip.hipStreamDestroy(h)
+
+
+def test_per_thread_default_stream_from_two_threads():
+    # hipStreamPerThread is one handle for a different stream on every host thread, so it
+    # gets no counters (second launch); two threads calling on it at once are both exact
+    import threading
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    M, N, K = 16, 4096, 8192
+    a, b = operands("fp16", M, N, K, 1, seed=11)
+    ref = cmpext3.fp16_matmul(a[0], b[0])
+    need = cabi.lib().cmpext3_gemm_workspace_size(cabi.F16, cabi.B_KN, M, N, K, 1)
+    outs = [torch.full((M, N), float("nan"), dtype=torch.float16, device="cuda") for _ in range(2)]
+    wss = [torch.empty(need, dtype=torch.uint8, device="cuda") for _ in range(2)]
+    torch.cuda.synchronize()
+    status = [None, None]
+
+    def work(i):
+        torch.cuda.set_device(0)
+        st = 0
+        for _ in range(20):
+            st = st or cabi.lib().cmpext3_gemm_ex(cabi.F16, cabi.B_KN, a[0].data_ptr(), K, 0, b[0].data_ptr(), N, 0,
+                                                  outs[i].data_ptr(), N, 0, None, M, N, K, 1, wss[i].data_ptr(),
+                                                  need, 2)  # hipStreamPerThread
+        status[i] = st or hip.hipStreamSynchronize(2)
+
+    ts = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    torch.cuda.synchronize()
+    assert status == [0, 0]
+    for c in outs:
+        assert torch.equal(c, ref)
