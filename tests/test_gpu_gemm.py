@@ -180,6 +180,8 @@ SPLIT_CASES = [
     # dtype, layout, M, N, K, ldc, batch, stride_c, bias
     ("fp16", "NK", 256, 1028, 8192, 1028, 1, 0, False),            # 128x128 tiles, 4 columns, 8-byte stores
     ("bf16", "KN", 16, 1024, 8192, 1027, 1, 0, True),              # skinny_wide, odd pitch
+    ("bf16", "KN", 16, 8000, 8192, 8003, 1, 0, True),              # skinny_wide, half a strip, element stores
+    ("fp16", "KN", 20, 8192, 8192, 8192, 1, 0, True),              # skinny_wide, 2 row blocks, 8-byte stores
     ("fp16", "KN", 16, 1024, 8192, 1024, 3, 16 * 1024 + 4, False),  # batch stride off the 16-byte grid
     ("fp16", "KN", 256, 4096, 4096, 4100, 1, 0, True),             # 128x128 tiles, pitch off the grid
     ("bf16", "NK", 256, 2052, 4096, 2052, 1, 0, True),             # W as [N, K], 4 columns per thread

@@ -42,6 +42,9 @@ CASES = [
     ("fp16", 40, 2056, 6144, 1),
     ("bf16", 64, 1024, 16384, 2),
     ("fp16", 8, 3000, 8192, 3),
+    ("fp16", 32, 8000, 8192, 1),
+    ("bf16", 16, 4096, 4352, 2),
+    ("bf16", 3, 8192, 8192, 1),
 ]
 
 
