@@ -33,11 +33,16 @@ thread count and ISA.  When the two rates differ by more than 0.8..1.25 the
 rate is not a property of the op at that size: `value` is then null and
 `null_reason` says so.
 
-power: after every workload's timed steps, the same op runs back to back for
---power-window seconds (default 1) while board power and shader clock (amdsmi
-gpu_metrics) are read; MFMA-bound rooflines also carry the fraction of the
-matrix peak at that sustained clock (`frac_at_sustained_sclk`; the nominal
-`frac` is the record).  torch_same_device: the same op through torch on the
+power (and settling): right before every workload's W warm-up calls, the same
+op runs back to back for --power-window seconds (default 1) while board power
+and shader clock (amdsmi gpu_metrics) are read.  A matrix-core-bound op that
+starts after other work runs 10-25 % slower for its first ~0.1-1 s while the
+board's power management settles (fp32 4097 x 3001 x 2049 on MI355X: 482 us per
+call with 5 warm-up calls, 405 with 50, 389 with 300), so without this window a
+short timed region measures that transient; with it, the K timed calls follow a
+second of the same op and the power and clock readings describe the state they
+run in.  MFMA-bound rooflines also carry the fraction of the matrix peak at that
+clock (`frac_at_sustained_sclk`; the nominal `frac` is the record).  torch_same_device: the same op through torch on the
 same GPU, timed the same way, as the reference's own harness compares
 (context, not the measured path).
 
@@ -89,9 +94,11 @@ HEADLINE = "cfg2_fp16_4096"
 # after the HBM-bound skinny config: successive calls 549, 449, 475, 508, 496 .. then
 # 390 us after a second; bf16 4096 x 14336 x 4096 after the 1x1 convolution: 366 .. 387,
 # then 330 us), so with few warm-up calls the timed steps would sit in that transient.
-# The HBM-bound workloads go first, then the fp32 ones, then the 16-bit ones, each
-# group from the least to the most sensitive, so that every matrix-core-bound workload
-# follows another of its kind.
+# Each workload therefore runs back to back for the power window (1 s by default) right
+# before its warm-up calls.  The order also helps when that window is off: the HBM-bound
+# workloads go first, then the fp32 ones, then the 16-bit ones, each group from the least
+# to the most sensitive, so that every matrix-core-bound workload follows another of its
+# kind.
 ORDER = ["cfg4_fp16_skinny", "conv1x1_fp16_64x128x128x128", "linear_fp32_4096", "bmm_fp32_16x1024",
          "cfg5_fp32_ragged", "linear_fp16_4096", "linear_bf16_4096", "bmm_fp16_16x1024", "bmm_bf16_16x1024",
          "cfg3_bf16_mlp", "cfg2_fp16_4096"]
@@ -238,7 +245,7 @@ class PowerClock:
                 "limit_residency": limits or None, "throttle_status": throttle or None,
                 "source": "amdsmi gpu_metrics (current_socket_power; current_gfxclks averaged over the XCDs), "
                           "one sample per firmware refresh, read while the same op ran back to back for "
-                          "window_s right after its timed steps"}
+                          "window_s right before its warm-up and timed calls"}
 
 
 POWER = None
@@ -303,19 +310,25 @@ def timed_region(fn, steps: int, warmup: int, label: str = "") -> tuple[float, f
 TIMED_REGIONS: list = []
 
 
-def power_window(fn, kern_ms: float, window_s: float) -> dict:
+def power_window(fn, window_s: float) -> dict:
     """The call back to back for `window_s` seconds while board power, shader clock and
     the firmware's limiter residencies are read (a timed region of a few ms is too
-    short for the firmware's metrics table to refresh inside it).  Run after every
-    workload's timed steps, so that its heat does not shape the next timed region."""
+    short for the firmware's metrics table to refresh inside it).  Run right before a
+    workload's warm-up and timed calls, so that those run in the settled state that
+    the readings describe.  Without amdsmi the calls still run (the settling does not
+    depend on the readings)."""
     import torch
 
     pc = power_clock()
-    if window_s <= 0 or pc.handle is None:
-        return pc.summary([], 0.0) if pc.handle is None else {"samples": 0, "error": "window disabled"}
+    if window_s <= 0:
+        return {"samples": 0, "error": "window disabled"}
     stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    fn(0)
+    torch.cuda.synchronize()
+    per = max(1, int(0.020 / max(time.perf_counter() - t, 1e-6)))  # batches of ~20 ms, two in flight
     samples, pending = [], []
-    per = max(1, int(20.0 / max(kern_ms, 1e-3)))  # batches of ~20 ms, two in flight
     w0 = time.perf_counter()
     i = 0
     while time.perf_counter() - w0 < window_s or pending:
@@ -327,7 +340,9 @@ def power_window(fn, kern_ms: float, window_s: float) -> dict:
             ev.record(stream)
             pending.append(ev)
         if len(pending) >= 2 or time.perf_counter() - w0 >= window_s:
-            pc.sample_until(pending.pop(0), float("inf"), samples)
+            ev = pending.pop(0)
+            pc.sample_until(ev, float("inf"), samples)
+            ev.synchronize()
     torch.cuda.synchronize()
     return pc.summary(samples, time.perf_counter() - w0)
 
@@ -375,7 +390,7 @@ def prepare_inputs(names) -> None:
     torch.cuda.synchronize()
 
 
-def time_gpu(name: str, steps: int, warmup: int, with_torch: bool = True) -> dict:
+def time_gpu(name: str, steps: int, warmup: int, with_torch: bool = True, window_s: float = 0.0) -> dict:
     import torch
 
     import cmpext3
@@ -385,11 +400,12 @@ def time_gpu(name: str, steps: int, warmup: int, with_torch: bool = True) -> dic
     prepare_inputs([name])
     a, bs = INPUTS[name]
     nb = len(bs)
+    power = power_window(lambda i: fn(a, bs[i % nb]), window_s)
     wall_ms, event_ms, kern_ms = timed_region(lambda i: fn(a, bs[i % nb]), steps, warmup, name)
     plan = cmpext3.last_plan()
     flops, nbytes = algorithmic(c)
     r = dict(config=name, desc=c["desc"], dtype=c["dtype"], kernel=plan.split()[0].split("=")[1], plan=plan,
-             power=None, ms_per_step=wall_ms, kernel_ms=kern_ms, event_ms_per_step=event_ms,
+             power=power, ms_per_step=wall_ms, kernel_ms=kern_ms, event_ms_per_step=event_ms,
              tflops=flops / (wall_ms * 1e-3) / 1e12, kernel_tflops=flops / (kern_ms * 1e-3) / 1e12,
              gbs=nbytes / (wall_ms * 1e-3) / 1e9, kernel_gbs=nbytes / (kern_ms * 1e-3) / 1e9)
     if with_torch:
@@ -397,8 +413,6 @@ def time_gpu(name: str, steps: int, warmup: int, with_torch: bool = True) -> dic
                               name + " (torch)")
         t["speedup"] = round(t["kernel_ms"] / kern_ms, 3)
         r["torch_same_device"] = t
-    # run later (power_window), after every workload's timed steps; keeps the inputs alive
-    r["power_job"] = lambda window_s: power_window(lambda i: fn(a, bs[i % nb]), kern_ms, window_s)
     return r
 
 
@@ -444,7 +458,7 @@ def caller_fn(c, cm):
     return lambda x, w, b: cm.conv2d(x, w, b)
 
 
-def time_caller(name: str, steps: int, warmup: int, with_torch: bool = True) -> dict:
+def time_caller(name: str, steps: int, warmup: int, with_torch: bool = True, window_s: float = 0.0) -> dict:
     import torch
     import torch.nn.functional as F
 
@@ -454,6 +468,7 @@ def time_caller(name: str, steps: int, warmup: int, with_torch: bool = True) -> 
     prepare_inputs([name])
     args = INPUTS[name]
     fn = caller_fn(c, cmpext3)
+    power = power_window(lambda i: fn(*args), window_s)
     wall_ms, event_ms, kern_ms = timed_region(lambda i: fn(*args), steps, warmup, name)
     flops, nbytes = caller_algorithmic(c)
     plan = cmpext3.last_plan()
@@ -473,9 +488,9 @@ def time_caller(name: str, steps: int, warmup: int, with_torch: bool = True) -> 
             unit: round(val, 2),
             "roofline": {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
                          "frac": round(ach / peak, 4), "traffic": load_traffic(name), "kernel": kernel,
-                         "kernel_ms": round(kern_ms, 5), "event_ms_per_step": round(event_ms, 5)},
-            "power": None, **({"torch_same_device": ref} if ref else {}),
-            "power_job": lambda window_s: power_window(lambda i: fn(*args), kern_ms, window_s)}
+                         "kernel_ms": round(kern_ms, 5), "event_ms_per_step": round(event_ms, 5),
+                         **clock_normalised(ach, peak, bound, power)},
+            "power": power, **({"torch_same_device": ref} if ref else {})}
 
 
 def cpu_description() -> str:
@@ -561,9 +576,12 @@ def rate_summary(rates: dict, unit: str, what: str, units: str = "rows") -> dict
 
 
 def cpu_caller(name: str, budget_s: float = 6.0) -> dict:
-    """The same caller on CPU tensors (torch.nn.functional.linear, torch.bmm,
-    torch.nn.functional.conv2d): rows of x (linear), rows of batch entry 0's A (bmm),
-    or whole images (conv)."""
+    """The same caller on CPU tensors: torch.nn.functional.linear on rows of x,
+    torch.bmm on rows of batch entry 0's A, and the 1x1 convolution on whole images
+    as the product it is, one 2-D torch.addmm per image, b + W[Cout, Cin] @ x[i][Cin, H*W]
+    (on the GPU box's host, torch.nn.functional.conv2d in fp16 took ~3.5 s per call for
+    one image and for two alike, and a batched fp16 torch.matmul ~2.5 s per image,
+    while the 2-D fp16 product behind F.linear runs at ~0.5 TFLOP/s)."""
     import torch
     import torch.nn.functional as F
 
@@ -580,13 +598,16 @@ def cpu_caller(name: str, budget_s: float = 6.0) -> dict:
         if c["op"] == "bmm":
             torch.bmm(args[0][:1, :n], args[1][:1])
             return 2.0 * n * N * K / 1e12
-        F.conv2d(args[0][:n], args[1], args[2])
+        w2, b2 = args[1].reshape(M, K), args[2].reshape(M, 1)
+        for i in range(n):
+            torch.addmm(b2, w2, args[0][i].reshape(K, -1))
         # bytes of the sample: its images in and out, the weight and the bias (GB)
         return esz * (n * N * K + n * N * M + M * K + M) / 1e9
 
     what = {"linear": f"F.linear on CPU ({c['dtype']}): x rows @ the full W^T + b",
             "bmm": f"torch.bmm on CPU ({c['dtype']}): rows of batch entry 0 @ its full B",
-            "conv": f"F.conv2d 1x1 on CPU ({c['dtype']}): whole images"}[c["op"]]
+            "conv": f"1x1 conv2d on CPU ({c['dtype']}) as b + W[Cout,Cin] @ x[i][Cin,H*W] "
+                    "(torch.addmm per image): whole images"}[c["op"]]
     log(f"cpu baseline {name}")
     return rate_summary(sample_rate(run, limit, budget_s), "GB/s" if c.get("hbm") else "TFLOP/s", what,
                         "images" if c["op"] == "conv" else "rows")
@@ -645,7 +666,8 @@ def load_traffic(name: str):
 
 def clock_normalised(ach: float, peak: float, bound: str, pwr: dict) -> dict:
     """For MFMA-bound work: the fraction of the matrix peak at the shader clock
-    measured during the timed steps (peak x sclk / 2400 MHz); the nominal `frac`
+    read over the window of back-to-back calls that precedes the timed steps
+    (peak x sclk / 2400 MHz); the nominal `frac`
     stays the record."""
     sclk = pwr.get("avg_sclk_mhz") if pwr else None
     if bound != "mfma" or not sclk:
@@ -661,7 +683,8 @@ def roofline(r: dict, name: str) -> dict:
         ach, peak, unit, bound = r["kernel_tflops"], PEAK[c["dtype"]], "TFLOP/s", "mfma"
     return {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
             "frac": round(ach / peak, 4), "traffic": load_traffic(name), "kernel": r["kernel"],
-            "kernel_ms": round(r["kernel_ms"], 5), "event_ms_per_step": round(r["event_ms_per_step"], 5)}
+            "kernel_ms": round(r["kernel_ms"], 5), "event_ms_per_step": round(r["event_ms_per_step"], 5),
+            **clock_normalised(ach, peak, bound, r["power"])}
 
 
 def main() -> int:
@@ -682,8 +705,9 @@ def main() -> int:
     ap.add_argument("--order", default=",".join(ORDER),
                     help="comma-separated order in which the configs and callers are timed")
     ap.add_argument("--power-window", type=float, default=POWER_WINDOW_S, metavar="S",
-                    help="after each workload's timed steps, run it back to back for S seconds while reading "
-                         "board power and shader clock (0: skip)")
+                    help="before each workload's warm-up and timed calls, run it back to back for S seconds "
+                         "while reading board power and shader clock, so that the timed calls run in that "
+                         "settled state (0: skip)")
     ap.add_argument("--caller", default=None, choices=sorted(CALLERS),
                     help="time only this caller and print its JSON object (for profiling)")
     ap.add_argument("--conv-shape", default=None, metavar="B,CIN,H,W,COUT",
@@ -748,15 +772,14 @@ def main() -> int:
         args.caller = name
     if args.caller:
         log(f"timing {args.caller} ({args.warmup} warm-up + {args.steps} steps)")
-        r = time_caller(args.caller, args.steps, args.warmup, not args.no_torch)
-        r.pop("power_job")
+        r = time_caller(args.caller, args.steps, args.warmup, not args.no_torch, args.power_window)
         print(json.dumps({args.caller: r}), flush=True)
         return 0
     with_torch = not args.no_torch
 
     def headline():
         log(f"timing {args.config} ({args.warmup} warm-up + {args.steps} steps)")
-        r = time_gpu(args.config, args.steps, args.warmup, with_torch)
+        r = time_gpu(args.config, args.steps, args.warmup, with_torch, args.power_window)
         log(f"{args.config}: {r['ms_per_step']:.4f} ms/step, {r['tflops']:.1f} TFLOP/s, {r['gbs']:.0f} GB/s")
         return r
 
@@ -776,11 +799,11 @@ def main() -> int:
     def time_one(name):
         if name in CALLERS:
             log(f"timing {name}")
-            callers[name] = time_caller(name, args.steps, args.warmup, with_torch)
+            callers[name] = time_caller(name, args.steps, args.warmup, with_torch, args.power_window)
             log(f"{name}: {callers[name]['ms_per_step']:.4f} ms/step")
             return
         log(f"timing {name}")
-        r = time_gpu(name, args.steps, args.warmup, with_torch)
+        r = time_gpu(name, args.steps, args.warmup, with_torch, args.power_window)
         log(f"{name}: {r['ms_per_step']:.4f} ms/step, {r['tflops']:.1f} TFLOP/s, {r['gbs']:.0f} GB/s")
         c = CONFIGS[name]
         others[name] = {"desc": r["desc"], **({"provenance": c["provenance"]} if "provenance" in c else {}),
@@ -788,9 +811,8 @@ def main() -> int:
                         "ms_per_step": round(r["ms_per_step"], 5),
                         **({"GB/s": round(r["gbs"], 1)} if c.get("hbm") else
                            {"TFLOP/s": round(r["tflops"], 2)}),
-                        "roofline": roofline(r, name), "power": None,
-                        **({"torch_same_device": r["torch_same_device"]} if with_torch else {}),
-                        "power_job": r["power_job"]}
+                        "roofline": roofline(r, name), "power": r["power"],
+                        **({"torch_same_device": r["torch_same_device"]} if with_torch else {})}
 
     callers = {}
     if not args.no_others:
@@ -821,17 +843,8 @@ def main() -> int:
         "config": {"workload": f"{args.config}: {c['desc']}", "M": c["M"], "N": c["N"], "K": c["K"],
                    "accumulate": "fp32", "kernel": head["kernel"], "plan": head["plan"]},
         "roofline": roofline(head, args.config),
-        "power": None,
+        "power": head["power"],
     }
-    # power and clock of every workload, each over a window of back-to-back calls, now that
-    # all timed regions are done
-    jobs = [(line, head["power_job"])] + [(o, o.pop("power_job")) for o in others.values()] + \
-           [(cl, cl.pop("power_job")) for cl in callers.values()]
-    for obj, job in jobs:
-        obj["power"] = job(args.power_window)
-        obj["roofline"].update(clock_normalised(obj["roofline"]["achieved"], obj["roofline"]["peak"],
-                                                obj["roofline"]["bound"], obj["power"]))
-    del jobs, head["power_job"]
     torch.cuda.empty_cache()
     if with_torch:
         line["torch_same_device"] = head["torch_same_device"]
