@@ -40,10 +40,11 @@ starts after other work runs 10-25 % slower for its first ~0.1-1 s while the
 board's power management settles (fp32 4097 x 3001 x 2049 on MI355X: 482 us per
 call with 5 warm-up calls, 405 with 50, 389 with 300), so without this window a
 short timed region measures that transient; with it, the K timed calls follow a
-second of the same op and the power and clock readings describe the state they
-run in.  MFMA-bound rooflines also carry the fraction of the matrix peak at that
-clock (`frac_at_sustained_sclk`; the nominal `frac` is the record).  torch_same_device: the same op through torch on the
-same GPU, timed the same way, as the reference's own harness compares
+second of the same op and the power and clock readings (averaged over the
+window's second half) describe the state they run in.  MFMA-bound rooflines also
+carry the fraction of the matrix peak at that clock (`frac_at_sustained_sclk`;
+the nominal `frac` is the record).  torch_same_device: the same op through torch
+on the same GPU, timed the same way, as the reference's own harness compares
 (context, not the measured path).
 
 callers: the reference callers on the GEMM path, at the shapes of the
@@ -205,16 +206,18 @@ class PowerClock:
                 self.error = f"{type(e).__name__}: {e}"
                 return
 
-    def summary(self, samples: list, window_s: float = 0.0) -> dict:
+    def summary(self, samples: list, window_s: float = 0.0, since: float = 0.0) -> dict:
+        """One sample per firmware refresh, from those read at or after `since`
+        (perf_counter seconds); the first sample read is dropped (its table may predate
+        the window)."""
         if self.handle is None or not samples:
             return {"samples": 0, "error": self.error or "no sample fell inside the window"}
-        # the firmware refreshes the table every few ms to seconds: keep one sample per refresh
-        # (the first sample is dropped: its table may predate the window)
         fresh, seen = [], {samples[0]["stamp"]}
         for x in samples[1:]:
             if x["stamp"] not in seen:
                 seen.add(x["stamp"])
-                fresh.append(x)
+                if x["t"] >= since:
+                    fresh.append(x)
         if not fresh:
             return {"samples": 0, "reads": len(samples),
                     "error": "the firmware's metrics table did not refresh during the window"}
@@ -241,11 +244,12 @@ class PowerClock:
                 "avg_power_w": round(statistics.mean(pw), 1) if pw else None,
                 "avg_sclk_mhz": round(statistics.mean(clk), 1) if clk else None,
                 "xcd_sclk_mhz_range": [round(min(lo)), round(max(hi))] if lo else None,
-                "window_s": round(window_s, 3),
+                "window_s": round(window_s, 3), "read_over": "the window's second half",
                 "limit_residency": limits or None, "throttle_status": throttle or None,
                 "source": "amdsmi gpu_metrics (current_socket_power; current_gfxclks averaged over the XCDs), "
                           "one sample per firmware refresh, read while the same op ran back to back for "
-                          "window_s right before its warm-up and timed calls"}
+                          "window_s right before its warm-up and timed calls, averaged over the window's second "
+                          "half (the first holds the clock's move from the previous workload's state)"}
 
 
 POWER = None
@@ -315,8 +319,10 @@ def power_window(fn, window_s: float) -> dict:
     the firmware's limiter residencies are read (a timed region of a few ms is too
     short for the firmware's metrics table to refresh inside it).  Run right before a
     workload's warm-up and timed calls, so that those run in the settled state that
-    the readings describe.  Without amdsmi the calls still run (the settling does not
-    depend on the readings)."""
+    the readings describe.  The readings come from the window's second half; the
+    firmware refreshes its table about once a second (MI355X), so the window runs on,
+    up to twice its length, until one refresh has landed there.  Without amdsmi the
+    calls still run for `window_s` (the settling does not depend on the readings)."""
     import torch
 
     pc = power_clock()
@@ -330,21 +336,33 @@ def power_window(fn, window_s: float) -> dict:
     per = max(1, int(0.020 / max(time.perf_counter() - t, 1e-6)))  # batches of ~20 ms, two in flight
     samples, pending = [], []
     w0 = time.perf_counter()
+    half, limit = w0 + window_s / 2, w0 + 2 * window_s
+    stamp_half = None  # the table's stamp when the second half began
+
+    def refreshed() -> bool:
+        return stamp_half is not None and any(x["stamp"] != stamp_half for x in samples if x["t"] >= half)
+
     i = 0
-    while time.perf_counter() - w0 < window_s or pending:
-        if time.perf_counter() - w0 < window_s:
+    while True:
+        now = time.perf_counter()
+        if stamp_half is None and now >= half:
+            stamp_half = samples[-1]["stamp"] if samples else -1
+        running = now - w0 < window_s or (pc.handle is not None and now < limit and not refreshed())
+        if not running and not pending:
+            break
+        if running:
             for _ in range(per):
                 fn(i)
                 i += 1
             ev = torch.cuda.Event()
             ev.record(stream)
             pending.append(ev)
-        if len(pending) >= 2 or time.perf_counter() - w0 >= window_s:
+        if len(pending) >= 2 or not running:
             ev = pending.pop(0)
             pc.sample_until(ev, float("inf"), samples)
             ev.synchronize()
     torch.cuda.synchronize()
-    return pc.summary(samples, time.perf_counter() - w0)
+    return pc.summary(samples, time.perf_counter() - w0, since=half)
 
 
 def make_cpu_inputs(c, nb: int, seed: int = 0):
