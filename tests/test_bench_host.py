@@ -53,3 +53,14 @@ def test_sample_rate_sizes():
     assert sorted(r) == [32, 64]
     r = bench.sample_rate(run, 16, 0.0, whole=True)
     assert list(r) == [16] and r[16][2] >= 2
+
+
+def test_cpu_conv_baseline_is_the_convolution():
+    # the CPU baseline's per-image product is the 1x1 convolution (float32, so exact enough)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 8, 5, 7, generator=g)
+    w = torch.randn(6, 8, 1, 1, generator=g)
+    b = torch.randn(6, generator=g)
+    ref = torch.nn.functional.conv2d(x, w, b)
+    got = bench.conv1x1_cpu(x, w, b)
+    assert got.shape == ref.shape and torch.allclose(got, ref, rtol=1e-5, atol=1e-5)
