@@ -600,8 +600,10 @@ def conv1x1_cpu(x, w, b):
 
     cout, cin = w.shape[0], w.shape[1]
     w2, b2 = w.reshape(cout, cin), b.reshape(cout, 1)
-    return torch.stack([torch.addmm(b2, w2, x[i].reshape(cin, -1)) for i in range(x.shape[0])]).reshape(
-        x.shape[0], cout, *x.shape[2:])
+    out = torch.empty((x.shape[0], cout, *x.shape[2:]), dtype=x.dtype)
+    for i in range(x.shape[0]):
+        torch.addmm(b2, w2, x[i].reshape(cin, -1), out=out[i].view(cout, -1))
+    return out
 
 
 def cpu_caller(name: str, budget_s: float = 6.0) -> dict:
