@@ -72,9 +72,9 @@ def plan(dtype: int, layout: int, M: int, N: int, K: int, lda: int | None = None
     lda = max(K, 1) if lda is None else lda
     ldb = max(N if layout == B_KN else K, 1) if ldb is None else ldb
     ldc = max(N, 1) if ldc is None else ldc
-    buf = ctypes.create_string_buffer(256)
+    buf = ctypes.create_string_buffer(640)
     kid = lib().cmpext3_gemm_plan(dtype, layout, M, N, K, lda, ldb, ldc, align, int(has_bias), batch,
-                                  workspace_bytes, buf, 256)
+                                  workspace_bytes, buf, 640)
     return kid, buf.value.decode()
 
 
@@ -132,8 +132,8 @@ def call_workspace_size(call: Call) -> int:
 
 
 def describe(call: Call) -> tuple[int, str]:
-    buf = ctypes.create_string_buffer(256)
-    kid = lib().cmpext3_gemm_call_describe(ctypes.byref(call), buf, 256)
+    buf = ctypes.create_string_buffer(640)
+    kid = lib().cmpext3_gemm_call_describe(ctypes.byref(call), buf, 640)
     return kid, buf.value.decode()
 
 

@@ -111,6 +111,16 @@ hipError_t dispatch(const Plan& plan, int dtype, int layout, const GemmParams& p
   }
 }
 
+// A plan's description; for a row split, both launches'.
+std::string describe_rows(const Request& r, const Plan& plan, int64_t m_main, const Plan& tail) {
+  if (m_main <= 0) return describe(r, plan);
+  Request head = r, rest = r;
+  head.M = m_main;
+  rest.M = r.M - m_main;
+  return describe(head, plan) + " rows=" + std::to_string(m_main) + " | rows " + std::to_string(m_main) + ".." +
+         std::to_string(r.M - 1) + ": " + describe(rest, tail);
+}
+
 constexpr int64_t kMaxGridZ = 65535;
 constexpr uint64_t kCallMagic = 0x636d7065787433ull;  // "cmpext3"
 
@@ -119,6 +129,9 @@ struct Prepared {
   uint64_t magic;
   Request r;
   Plan plan;
+  // rows [0, m_main) run with `plan`, the rest with `tail` (0: one launch for all rows)
+  int64_t m_main;
+  Plan tail;
   const void* A;
   const void* B;
   void* C;
@@ -164,6 +177,12 @@ int prepare(Prepared* pc, int dtype, int b_layout, const void* A, int64_t lda, i
   p.magic = kCallMagic;
   p.r = r;
   p.plan = plan;
+  RowSplit rs;
+  if (!empty && plan_row_split(r, plan, &rs)) {
+    p.plan = rs.main;
+    p.m_main = rs.m_main;
+    p.tail = rs.tail;
+  }
   p.A = A;
   p.B = B;
   p.C = C;
@@ -185,6 +204,19 @@ const Prepared* as_prepared(const cmpext3_gemm_call* call) {
 int run(const Prepared& pc, void* workspace, int64_t workspace_bytes, hipStream_t s) {
   const Plan& plan = pc.plan;
   if (pc.empty) return CMPEXT3_OK;
+  if (pc.m_main > 0) {  // two launches over the rows, one after the other on the stream
+    const int64_t esz = pc.r.dtype == kF32 ? 4 : 2;
+    Prepared head = pc, rest = pc;
+    head.m_main = rest.m_main = 0;
+    head.r.M = pc.m_main;
+    rest.r.M = pc.r.M - pc.m_main;
+    rest.plan = pc.tail;
+    rest.A = (const char*)pc.A + pc.m_main * pc.r.lda * esz;
+    rest.C = (char*)pc.C + pc.m_main * pc.r.ldc * esz;
+    if (pc.bias != nullptr && pc.bias_row) rest.bias = (const char*)pc.bias + pc.m_main * esz;
+    const int st = run(head, workspace, workspace_bytes, s);
+    return st != CMPEXT3_OK ? st : run(rest, workspace, workspace_bytes, s);
+  }
   if (plan.ws_bytes > 0 && (workspace == nullptr || align_of(workspace) < 16 || workspace_bytes < plan.ws_bytes))
     return CMPEXT3_ERR_WORKSPACE;
   const int dtype = pc.r.dtype, b_layout = pc.r.layout;
@@ -292,14 +324,16 @@ extern "C" int cmpext3_gemm_prepare(cmpext3_gemm_call* call, int dtype, int b_la
 
 extern "C" int64_t cmpext3_gemm_call_workspace_size(const cmpext3_gemm_call* call) {
   const Prepared* pc = as_prepared(call);
-  return pc ? pc->plan.ws_bytes : (int64_t)CMPEXT3_ERR_INVALID_ARG;
+  if (pc == nullptr) return (int64_t)CMPEXT3_ERR_INVALID_ARG;
+  // the two launches of a row split share the workspace, one after the other
+  return pc->m_main > 0 ? std::max(pc->plan.ws_bytes, pc->tail.ws_bytes) : pc->plan.ws_bytes;
 }
 
 extern "C" int cmpext3_gemm_call_describe(const cmpext3_gemm_call* call, char* buf, int buflen) {
   const Prepared* pc = as_prepared(call);
   if (pc == nullptr) return CMPEXT3_ERR_INVALID_ARG;
   if (buf && buflen > 0) {
-    const std::string d = describe(pc->r, pc->plan);
+    const std::string d = describe_rows(pc->r, pc->plan, pc->m_main, pc->tail);
     strncpy(buf, d.c_str(), (size_t)buflen - 1);
     buf[buflen - 1] = '\0';
   }
@@ -386,7 +420,9 @@ extern "C" int64_t cmpext3_gemm_workspace_size(int dtype, int b_layout, int M, i
                                  batch, INT64_MAX);
   Plan plan;
   const int st = make_plan(r, &plan);
-  return st == CMPEXT3_OK ? plan.ws_bytes : (int64_t)st;
+  if (st != CMPEXT3_OK) return st;
+  RowSplit rs;
+  return plan_row_split(r, plan, &rs) ? std::max(rs.main.ws_bytes, rs.tail.ws_bytes) : plan.ws_bytes;
 }
 
 extern "C" int cmpext3_gemm_plan(int dtype, int b_layout, int M, int N, int K, int64_t lda, int64_t ldb,
@@ -396,12 +432,14 @@ extern "C" int cmpext3_gemm_plan(int dtype, int b_layout, int M, int N, int K, i
   Plan plan;
   const int st = make_plan(r, &plan);
   if (st != CMPEXT3_OK) return st;
+  RowSplit rs;
+  const bool split = M > 0 && N > 0 && batch > 0 && plan_row_split(r, plan, &rs);
   if (buf && buflen > 0) {
-    const std::string d = describe(r, plan);
+    const std::string d = split ? describe_rows(r, rs.main, rs.m_main, rs.tail) : describe(r, plan);
     strncpy(buf, d.c_str(), (size_t)buflen - 1);
     buf[buflen - 1] = '\0';
   }
-  return (int)plan.kernel;
+  return (int)(split ? rs.main.kernel : plan.kernel);
 }
 
 extern "C" const char* cmpext3_status_string(int status) {

@@ -342,7 +342,7 @@ std::string plan(const std::string& dtype, int64_t M, int64_t N, int64_t K, cons
                                                 : -1;
   const int lay = layout == "NK" ? CMPEXT3_B_NK : CMPEXT3_B_KN;
   const int64_t ldb = lay == CMPEXT3_B_KN ? N : K;
-  char buf[256];
+  char buf[640];
   // packed operands at 16-byte aligned addresses, and the workspace the plan asks for
   // (what the bindings provide); cmpext3.last_plan() reports what a call actually ran
   const int st = cmpext3_gemm_plan(code, lay, (int)M, (int)N, (int)K, std::max<int64_t>(K, 1),
@@ -354,7 +354,7 @@ std::string plan(const std::string& dtype, int64_t M, int64_t N, int64_t K, cons
 
 std::string last_plan() {
   TORCH_CHECK(g_has_last_call, "cmpext3.last_plan: no operator has run on this thread yet");
-  char buf[256];
+  char buf[640];
   const int st = cmpext3_gemm_call_describe(&g_last_call, buf, sizeof buf);
   TORCH_CHECK(st >= 0, "cmpext3.last_plan: ", cmpext3_status_string(st));
   return std::string(buf);

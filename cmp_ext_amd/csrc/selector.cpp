@@ -661,6 +661,69 @@ int make_plan(const Request& r, Plan* plan) {
 }
 
 
+// Modelled time (us) of a 16-bit plan, for comparing a row split with the plan it would
+// replace: the tile cost model above for the tiled kernels, and reading A and B and
+// writing C once at ~5 TB/s for the HBM-bound ones; ~2 us per launch.
+static double plan_us(const Request& r, const Plan& p) {
+  for (const Candidate& c : kTiles16)
+    if (c.id == p.kernel) return split_cost(c, r.M, r.N, r.K, r.batch, std::max(1, p.splits)) / kUnitsPerUs + 2.0;
+  const double b_copies = (r.batch > 1 && r.stride_b != 0) ? (double)r.batch : 1.0;
+  const double a_copies = (r.batch > 1 && r.stride_a != 0) ? (double)r.batch : 1.0;
+  const double bytes = 2.0 * (a_copies * r.M * r.K + b_copies * r.K * r.N + (double)r.batch * r.M * r.N);
+  return bytes / 5.0e6 + 3.0;
+}
+
+bool plan_row_split(const Request& r, const Plan& full, RowSplit* out) {
+  if ((r.dtype != kF16 && r.dtype != kBF16) || full.forced || full.pad_a || full.pad_b || r.M <= 256 ||
+      r.N == 0 || r.K == 0 || r.batch == 0)
+    return false;
+  const Candidate* fc = nullptr;
+  for (const Candidate& c : kTiles16)
+    if (c.id == full.kernel) fc = &c;
+  if (fc == nullptr) return false;
+  // Only a last round at most half full after at least one full round: a fuller last
+  // round runs at a higher clock than the model assumes (fewer busy CUs under the same
+  // power limit), and the split did not pay there (MI355X, fp16 2100 x 4096 x 4096: 171
+  // tiles of 256x224 in one partial round 69.9 us, split into 2048 rows of 128x128 and 52
+  // rows of skinny_wide 76.5 us).
+  const int64_t slots = (int64_t)kNumCUs * fc->occ;
+  const int64_t wgs = (int64_t)full.tiles_m * full.tiles_n * r.batch * std::max(1, full.splits);
+  const int64_t rem = wgs % slots;
+  if (wgs <= slots || rem == 0 || 2 * rem > slots) return false;
+  // rows covered by whole rounds of the 256-row tiles (one workgroup per CU), and whole 256-row tiles
+  int64_t cand[3] = {r.M / 256 * 256, 0, 0};
+  for (int i = 0; i < 2; ++i) {
+    const int64_t cols = cdiv(r.N, i == 0 ? 256 : 224) * r.batch;
+    if (cols <= kNumCUs) {
+      const int64_t rows = 256 * (kNumCUs / cols);
+      cand[1 + i] = r.M / rows * rows;
+    }
+  }
+  const double full_us = plan_us(r, full);
+  double best = 0.92 * full_us;
+  bool found = false;
+  for (int64_t m_main : cand) {
+    if (m_main <= 0 || m_main >= r.M) continue;
+    Request a = r, b = r;
+    a.M = m_main;
+    b.M = r.M - m_main;
+    // (the tail's A and C start m_main rows in: 16-byte aligned as the rows are, m_main
+    // being a multiple of 256)
+    Plan pa, pb;
+    if (make_plan(a, &pa) != CMPEXT3_OK || make_plan(b, &pb) != CMPEXT3_OK) continue;
+    if (pa.pad_a || pa.pad_b || pb.pad_a || pb.pad_b || pa.kernel == kGeneric16 || pb.kernel == kGeneric16) continue;
+    const double us = plan_us(a, pa) + plan_us(b, pb);
+    if (us < best) {
+      best = us;
+      out->m_main = m_main;
+      out->main = pa;
+      out->tail = pb;
+      found = true;
+    }
+  }
+  return found;
+}
+
 std::string describe(const Request& r, const Plan& p) {
   static const char* dt[] = {"f16", "bf16", "f32"};
   char buf[256];

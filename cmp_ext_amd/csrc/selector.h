@@ -49,6 +49,18 @@ struct Request {
 // Returns 0 and fills *plan, or a negative CMPEXT3_ERR_* code.
 int make_plan(const Request& r, Plan* plan);
 
+// A 16-bit tiled product whose last round of tiles would run mostly empty (rows just
+// past a multiple of what one round covers) runs as two launches over its rows: rows
+// [0, m_main) with `main`, the remaining rows with `tail` (each planned for its rows of
+// the same operands; they write disjoint rows of C).
+struct RowSplit {
+  int64_t m_main;
+  Plan main, tail;
+};
+// Given the plan for all rows, returns true and fills *out when the two launches are
+// modelled to take less than 0.92 of its time.
+bool plan_row_split(const Request& r, const Plan& full, RowSplit* out);
+
 // One-line description of a plan, e.g. "tile256x256 f16 KN grid=256x1".
 std::string describe(const Request& r, const Plan& p);
 

@@ -131,13 +131,18 @@ int cmpext3_conv2d_1x1(int dtype, const void* input, const void* weight, const v
  *
  * cmpext3_gemm_prepare validates the arguments (those of cmpext3_gemm_ex, plus
  * `flags`), picks the kernel and stores the whole call -- pointers, sizes and
- * the plan -- in *call; nothing is launched and no GPU is touched.
+ * the plan -- in *call; nothing is launched and no GPU is touched.  A 16-bit
+ * product whose last round of output tiles would run mostly empty (M just past
+ * what whole rounds of 256-row tiles cover) is planned as two launches over its
+ * rows, one for the rows whole rounds cover and one for the rest; they share the
+ * workspace, one after the other.
  * `workspace_limit` is the most workspace the caller is willing to provide
  * (0: none; INT64_MAX: whatever helps).  CMPEXT3_BIAS_PER_ROW in `flags` adds
  * the bias per row of C (M elements) instead of per column (N elements).
  * cmpext3_gemm_call_workspace_size says how much workspace the chosen kernels
  * need (<= workspace_limit), cmpext3_gemm_call_describe writes a one-line
- * description of them and returns the kernel id, and cmpext3_gemm_run
+ * description of them (up to ~600 characters for two launches) and returns the
+ * kernel id (of the first launch), and cmpext3_gemm_run
  * enqueues them on `stream` with a workspace of at least that many bytes
  * (16-byte aligned; NULL when none is needed; CMPEXT3_ERR_WORKSPACE otherwise).
  * A prepared call may be run more than once (e.g. while a graph is captured);
@@ -199,8 +204,8 @@ int64_t cmpext3_gemm_workspace_size(int dtype, int b_layout, int M, int N, int K
 
 /*
  * Kernel selection, host only (no GPU needed): writes a one-line description
- * of the kernel cmpext3_gemm_ex would launch for these arguments into buf and
- * returns the kernel id (>= 0) or a negative CMPEXT3_ERR_*.  `align` is the
+ * of the kernel(s) cmpext3_gemm_ex would launch for these arguments into buf and
+ * returns the kernel id (of the first launch; >= 0) or a negative CMPEXT3_ERR_*.  `align` is the
  * largest power of two (up to 16) dividing the byte address of every operand;
  * `workspace_bytes` is the workspace the call would provide.
  * No counterpart in the reference, whose tile choice is fixed at compile time

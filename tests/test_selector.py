@@ -339,3 +339,29 @@ def test_gemm_config_override(monkeypatch):
         assert desc == base or (bad.startswith("kernel=tile128x128") and "splits" not in desc), (bad, desc)
     monkeypatch.delenv("CMPEXT3_GEMM_CONFIG")
     assert cabi.plan(cabi.F16, cabi.B_KN, 2048, 2048, 2048, workspace_bytes=ws)[1] == base
+
+
+def test_row_split_of_mostly_empty_last_rounds():
+    # 4100 rows: whole 256x256 rounds for 4096 rows (one round), the 4 left over on the
+    # skinny kernel (split K with a workspace, narrow strips without)
+    kid, desc = cabi.plan(cabi.BF16, cabi.B_KN, 4100, 4096, 4096, workspace_bytes=1 << 30)
+    assert kid == K_TILE256 and "grid=16x16x1" in desc and " rows=4096 | rows 4096..4099: kernel=skinny_wide" in desc
+    kid, desc = cabi.plan(cabi.BF16, cabi.B_KN, 4100, 4096, 4096)
+    assert kid == K_TILE256 and " rows=4096 | rows 4096..4099: kernel=skinny " in desc, desc
+    kid, desc = cabi.plan(cabi.F16, cabi.B_NK, 4100, 4096, 4096, has_bias=True, workspace_bytes=1 << 30)
+    assert " rows=4096 | rows 4096..4099: kernel=skinny_nk" in desc, desc
+    kid, desc = cabi.plan(cabi.BF16, cabi.B_NK, 5000, 4096, 4096, workspace_bytes=1 << 30)
+    assert " rows=4096 | rows 4096..4999: kernel=tile128x128" in desc, desc
+    # the workspace the call asks for is the larger of the two launches' (they share it)
+    assert cabi.workspace_size(cabi.BF16, cabi.B_KN, 4100, 4096, 4096) == 8 * 4 * 4096 * 4
+    # whole rounds, a last round more than half full, or fp32: one launch
+    for dtype, M, N, K in [(cabi.F16, 4096, 4096, 4096), (cabi.F16, 2100, 4096, 4096),
+                           (cabi.BF16, 1030, 14336, 4096), (cabi.F32, 4100, 4096, 4096), (cabi.F16, 4100, 64, 4096)]:
+        _, desc = cabi.plan(dtype, cabi.B_KN, M, N, K, workspace_bytes=1 << 30)
+        assert " rows=" not in desc, desc
+
+
+def test_row_split_not_under_override(monkeypatch):
+    monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=tile128x128")
+    kid, desc = cabi.plan(cabi.BF16, cabi.B_KN, 4100, 4096, 4096, workspace_bytes=1 << 30)
+    assert kid == K_TILE128 and " rows=" not in desc, desc
