@@ -35,6 +35,29 @@ CASES = [
 ]
 
 
+def _random_split_cases(n, seed=11):
+    """Seeded random shapes (multiples of 8 in N and K) whose plan splits the rows."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        dtype = ["fp16", "bf16"][rng.integers(2)]
+        layout = ["KN", "NK"][rng.integers(2)]
+        batch = int(rng.choice([1, 1, 2]))
+        M, N, K = int(rng.integers(257, 7000)), int(rng.integers(1, 769)) * 8, int(rng.integers(1, 385)) * 8
+        if M * N * K * batch > 1.2e11:
+            continue
+        bias = [None, "col", "row"][rng.integers(3)]
+        ws = bool(rng.integers(2))
+        _, d = cabi.plan(CODE[dtype], cabi.B_KN if layout == "KN" else cabi.B_NK, M, N, K, ldc=N + 8,
+                         has_bias=bias is not None, batch=batch, workspace_bytes=(1 << 62) if ws else 0)
+        if " rows=" in d:
+            out.append((dtype, layout, M, N, K, batch, bias, ws))
+    return out
+
+
+CASES += _random_split_cases(8)
+
+
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "-".join(str(x) for x in c))
 def test_row_split(case):
     dtype, layout, M, N, K, batch, bias_mode, with_ws = case
