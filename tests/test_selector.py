@@ -365,3 +365,34 @@ def test_row_split_not_under_override(monkeypatch):
     monkeypatch.setenv("CMPEXT3_GEMM_CONFIG", "kernel=tile128x128")
     kid, desc = cabi.plan(cabi.BF16, cabi.B_KN, 4100, 4096, 4096, workspace_bytes=1 << 30)
     assert kid == K_TILE128 and " rows=" not in desc, desc
+
+
+def test_row_split_plans_cover_the_rows():
+    # random 16-bit shapes: where the plan splits the rows, the first launch covers a
+    # multiple of 256 rows short of M, the second the rest, and the workspace the call asks
+    # for is what both launches need (the larger of the two)
+    import numpy as np
+
+    rng = np.random.default_rng(3)
+    splits = 0
+    for _ in range(400):
+        dtype = [cabi.F16, cabi.BF16][rng.integers(2)]
+        layout = [cabi.B_KN, cabi.B_NK][rng.integers(2)]
+        M, N, K = int(rng.integers(1, 9000)), int(rng.integers(1, 1025)) * 8, int(rng.integers(1, 513)) * 8
+        batch = int(rng.choice([1, 2, 3]))
+        ws = int(rng.choice([0, 1 << 40]))
+        kid, desc = cabi.plan(dtype, layout, M, N, K, batch=batch, workspace_bytes=ws)
+        assert kid >= 0, desc
+        if " rows=" not in desc:
+            continue
+        splits += 1
+        m_main = int(desc.split(" rows=")[1].split()[0])
+        assert 0 < m_main < M and m_main % 256 == 0, desc
+        assert f" | rows {m_main}..{M - 1}: kernel=" in desc, desc
+        head, tail = desc.split(" rows=")[0], desc.split(": ", 1)[1]
+        _, head_alone = cabi.plan(dtype, layout, m_main, N, K, batch=batch, workspace_bytes=ws)
+        _, tail_alone = cabi.plan(dtype, layout, M - m_main, N, K, batch=batch, workspace_bytes=ws)
+        assert head == head_alone and tail == tail_alone, (desc, head_alone, tail_alone)
+        if ws == 0:
+            assert "workspace=" not in desc, desc
+    assert splits >= 10
