@@ -109,3 +109,31 @@ def test_row_split(case):
         elif bias_mode == "row":
             ref = ref + O.to_f64(bias)[rows][:, None]
         assert O.rel_frobenius(O.to_f64(out[i][rows]), ref) <= O.TOLERANCE[dtype], (i, desc)
+
+
+def test_row_split_under_graph_capture():
+    # the two launches captured in a graph (the skinny tail then sums its split-K partials in
+    # a second launch instead of in-kernel): every replay equals the eager result bit for bit
+    import cmpext3
+
+    g = torch.Generator().manual_seed(41)
+    a = (torch.randn(4100, 4096, generator=g) / 64).to(torch.bfloat16).cuda()
+    b = torch.randn(4096, 4096, generator=g).to(torch.bfloat16).cuda()
+    eager = cmpext3.bf16_matmul(a, b)
+    desc = cmpext3.last_plan()
+    assert " rows=4096 | rows 4096..4099: kernel=skinny_wide" in desc, desc
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        cmpext3.bf16_matmul(a, b)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = cmpext3.bf16_matmul(a, b)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert torch.equal(cmpext3.bf16_matmul(a, b), eager)
